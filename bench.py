@@ -1,0 +1,297 @@
+"""Benchmark: Q4 GEMV HBM GB/s at M=1 (the headline) plus Q4 GEMM TOPS at M=512.
+
+Headline workload (one "step"): the FFN-shaped Q4 decode GEMVs
+  up   K=1536 -> N=8192   and   down K=8192 -> N=1536,
+each launch reading a different copy of its weights from a rotating pool
+larger than 2x the 256 MB Infinity Cache, so the bytes come from HBM.
+x and y stay resident in HBM; fp32 x in, fp32 y out, activation
+quantization fused into the GEMV.
+
+value = algorithmic bytes / time, bytes = Q4 blocks as-is (18 B per 32
+weights) + 4*K (x) + 4*N (y) per GEMV.
+
+Also reported (one JSON line, under "extra"): the 16-layer decode sweep,
+ragged Q4 GEMM M in {4,16,64}, prefill Q4 GEMM M=512 / 2048 TOPS (fraction of
+int8 MFMA peak), Q8_0 GEMV K=N=1536 -- and, on rank 0, the CPU baseline: the
+oracle's runtime-dispatched llm-cpu restatement (VNNI-512 > AVX2 > scalar)
+timed on this host's cores over a bounded sample of the same GEMV workload.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5033.0        # MI355X dense int8 MFMA, TOPS (256 CU x 2.4 GHz x 8192)
+MALL_BYTES = 256 << 20
+METRIC = "Q4 GEMV HBM GB/s at M=1; Q4 GEMM TOPS at M=512 (frac. of roofline)"
+
+
+def q4_bytes(n, k, m=1):
+    return n * (k // 32) * 18 + 4 * k * m + 4 * n * m
+
+
+def q8_bytes(n, k, m=1):
+    return n * (k // 32) * 34 + 4 * k * m + 4 * n * m
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class GpuBench:
+    def __init__(self):
+        import torch
+
+        from llmhost_amd import q4
+
+        self.torch = torch
+        self.q4 = q4
+        self.ctx = q4.Context(0)
+        self.stream = torch.cuda.Stream()  # default priority
+        self.ctx.set_stream(self.stream.cuda_stream)
+
+    def copies(self, n, k, seed, min_bytes):
+        """Distinct device copies of one seeded Q4 matrix (uploaded once,
+        re-packed on the device from a device-resident block buffer)."""
+        from llmhost_amd import synth
+
+        blocks = synth.q4_blocks(seed, n, k)
+        raw = self.torch.from_numpy(blocks.view(np.uint8).copy()).cuda()
+        per = n * (k // 32) * 18
+        count = max(1, math.ceil(min_bytes / per))
+        mats = [self.q4.Q4Matrix.from_blocks(n, k, raw, self.ctx) for _ in range(count)]
+        del raw
+        return blocks, mats
+
+    def timed(self, fn, iters, warmup):
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for i in range(warmup):
+                fn(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            for i in range(iters):
+                fn(i)
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters  # ms per iteration
+
+
+def gemv_workload(gb: GpuBench, steps: int, warmup: int):
+    torch, q4 = gb.torch, gb.q4
+    shapes = {"up": (8192, 1536), "down": (1536, 8192)}
+    mats, xs, ys = {}, {}, {}
+    for i, (name, (n, k)) in enumerate(shapes.items()):
+        _, mats[name] = gb.copies(n, k, 101 + i, 2 * MALL_BYTES + (64 << 20))
+        from llmhost_amd import synth
+
+        xs[name] = torch.from_numpy(synth.normal_f32(201 + i, k)).cuda()
+        ys[name] = torch.zeros(n, device="cuda")
+    C = min(len(m) for m in mats.values())
+
+    def step(i):
+        q4.gemv_q4(mats["up"][i % C], xs["up"], ys["up"])
+        q4.gemv_q4(mats["down"][i % C], xs["down"], ys["down"])
+
+    ms = gb.timed(step, steps, warmup)
+    step_bytes = sum(q4_bytes(n, k) for n, k in shapes.values())
+    per_kernel = {}
+    for name, (n, k) in shapes.items():
+        def one(i, name=name):
+            q4.gemv_q4(mats[name][i % C], xs[name], ys[name])
+        kms = gb.timed(one, max(steps, 200), warmup)
+        per_kernel[name] = {"n": n, "k": k, "us": kms * 1e3, "bytes": q4_bytes(n, k),
+                            "gbs": q4_bytes(n, k) / (kms * 1e-3) / 1e9}
+    return ms, step_bytes, C, per_kernel, mats
+
+
+def decode_sweep(gb: GpuBench, iters: int):
+    """16 layers: qkv 1536->2048, o 1536->1536, gate/up pair 1536->8192, down 8192->1536 (AddF64)."""
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    H, F, L = 1536, 8192, 16
+    layers = []
+    raw_cache = {}
+    for layer in range(L):
+        mats = {}
+        for j, (name, n, k) in enumerate([("qkv", 2048, H), ("o", H, H), ("gate", F, H), ("up", F, H),
+                                          ("down", H, F)]):
+            key = (n, k, j)
+            if key not in raw_cache:
+                raw_cache[key] = torch.from_numpy(synth.q4_blocks(500 + j, n, k).view(np.uint8).copy()).cuda()
+            mats[name] = q4.Q4Matrix.from_blocks(n, k, raw_cache[key], gb.ctx)
+        layers.append(mats)
+    raw_cache.clear()
+    x = torch.from_numpy(synth.normal_f32(7, H)).cuda()
+    qkv = torch.zeros(2048, device="cuda")
+    h = torch.zeros(H, device="cuda")
+    g = torch.zeros(F, device="cuda")
+    u = torch.zeros(F, device="cuda")
+
+    def step(_):
+        for m in layers:
+            q4.gemv_q4(m["qkv"], x, qkv)
+            q4.gemv_q4(m["o"], x, h)
+            q4.gemv_q4_pair(m["gate"], m["up"], x, g, u)
+            q4.gemv_q4_add(m["down"], g, h)
+
+    ms = gb.timed(step, iters, 2)
+    total = L * (q4_bytes(2048, H) + q4_bytes(H, H) + 2 * q4_bytes(F, H) + q4_bytes(H, F))
+    for m in layers:
+        for w in m.values():
+            w.free()
+    return {"us": ms * 1e3, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9,
+            "frac_hbm": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "launches": 4 * L}
+
+
+def gemm_case(gb: GpuBench, m, n, k, iters, seed):
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    _, mats = gb.copies(n, k, seed, 2 * MALL_BYTES if m <= 64 else 1)
+    x = torch.from_numpy(synth.activations(seed + 1, m, k)).cuda()
+    y = torch.zeros(m, n, device="cuda")
+    C = len(mats)
+    ms = gb.timed(lambda i: q4.gemm_q4(mats[i % C], x, y, m), iters, 3)
+    ops = 2.0 * m * n * k
+    byts = q4_bytes(n, k, m)
+    for w in mats:
+        w.free()
+    return {"m": m, "n": n, "k": k, "us": ms * 1e3, "tops": ops / (ms * 1e-3) / 1e12,
+            "frac_int8": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "gbs": byts / (ms * 1e-3) / 1e9}
+
+
+def q8_case(gb: GpuBench, iters):
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    n = k = 1536
+    b8 = synth.q8_blocks(71, n, k)
+    count = math.ceil(2 * MALL_BYTES / (n * (k // 32) * 34))
+    mats = [q4.Q8Matrix.from_blocks(n, k, b8, gb.ctx) for _ in range(count)]
+    x = torch.from_numpy(synth.normal_f32(72, k)).cuda()
+    y = torch.zeros(n, device="cuda")
+    ms = gb.timed(lambda i: q4.q8_apply(mats[i % count], x, 1, y), iters, 10)
+    for w in mats:
+        w.free()
+    return {"us": ms * 1e3, "gbs": q8_bytes(n, k) / (ms * 1e-3) / 1e9}
+
+
+def cpu_baseline(target_s: float = 12.0):
+    """The oracle's llm-cpu restatement (runtime-dispatched kernel, pinned
+    pool) on this host, over rotating packed copies larger than the LLC."""
+    import oracle
+    from llmhost_amd import synth
+
+    threads = min(16, len(os.sched_getaffinity(0)), oracle.lib().oq_max_threads())
+    kern = oracle.detect_kernel()
+    shapes = [(8192, 1536), (1536, 8192)]
+    ncopies = 24  # 24 x 2 x 7.9 MB of packed CPU tiles, beyond a typical LLC
+    mats, xs = [], []
+    for i, (n, k) in enumerate(shapes):
+        blocks = synth.q4_blocks(101 + i, n, k)
+        mats.append([oracle.Q4Matrix(n, k, blocks) for _ in range(ncopies)])
+        xs.append(synth.normal_f32(201 + i, k))
+    outs = [np.zeros(n, dtype=np.float32) for n, _ in shapes]
+    for j in range(2):  # warm-up / page-in
+        for s in range(2):
+            oracle.gemv_q4(mats[s][j], xs[s], outs[s], threads=threads)
+    step_bytes = sum(q4_bytes(n, k) for n, k in shapes)
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        for s in range(2):
+            oracle.gemv_q4(mats[s][steps % ncopies], xs[s], outs[s], threads=threads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    gbs = steps * step_bytes / el / 1e9
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "kernel": oracle.kernel_name(kern),
+            "sample": f"{steps} steps (up 1536->8192 + down 8192->1536 Q4 GEMV, fp32 x in, act-quant "
+                      f"included) over {ncopies} rotating packed copies, {el:.1f} s wall",
+            "ms_per_step": el / steps * 1e3}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline GEMV only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the hot path is a "
+              "single-GPU kernel; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    gb = GpuBench()
+    log("[bench] headline GEMV workload")
+    ms, step_bytes, copies, per_kernel, _ = gemv_workload(gb, args.steps, args.warmup)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    dom = min(per_kernel.values(), key=lambda d: d["gbs"])
+    dom_name = [k for k, v in per_kernel.items() if v is dom][0]
+    extra = {"gemv_per_kernel": per_kernel, "weight_copies_per_shape": copies}
+    if not args.quick:
+        log("[bench] decode sweep")
+        extra["decode_sweep_16L"] = decode_sweep(gb, 10)
+        log("[bench] gemm cases")
+        for m in (4, 16, 64):
+            extra[f"ragged_gemm_m{m}"] = gemm_case(gb, m, 8192, 2048, 50, 300 + m)
+        for (m, n, k) in [(512, 10752, 2048), (512, 2048, 10752), (2048, 10752, 2048), (2048, 2048, 10752)]:
+            extra[f"prefill_gemm_m{m}_k{k}_n{n}"] = gemm_case(gb, m, n, k, 10, 400 + m + k)
+        log("[bench] q8 gemv")
+        extra["q8_gemv_k1536_n1536"] = q8_case(gb, 200)
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded SplitMix64: uniform Q4 nibbles, f16 scales U[1e-3,2e-2], x ~ N(0,1))",
+        "config": {"workload": "Q4 GEMV M=1: up K=1536,N=8192 + down K=8192,N=1536 per step, "
+                               f"{copies} rotating weight copies per shape (> 2x MALL)",
+                   "global_batch": 1, "seq_len": 1, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": f"q4_gemv ({dom_name}: K={dom['k']}, N={dom['n']})",
+                     "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    if "prefill_gemm_m512_k2048_n10752" in extra:
+        g = extra["prefill_gemm_m512_k2048_n10752"]
+        out["gemm_m512"] = {"tops": round(g["tops"], 2), "frac_int8_peak": round(g["frac_int8"], 4),
+                            "us": round(g["us"], 2)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

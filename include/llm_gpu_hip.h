@@ -1,0 +1,168 @@
+/*
+ * llm_gpu_hip.h -- C ABI of the MI355X (gfx950) block-quantized matmul library.
+ *
+ * Drop-in for llmhost's CPU matmul seam: the functions below replace the
+ * llm-cpu free functions that crates/llm-engine/src/weights.rs dispatches to
+ * (Linear::apply / apply_add / apply_pair, OutputHead::apply).  Each
+ * declaration cites the reference interface it replaces (paths relative to
+ * the llmhost repository root).
+ *
+ * Conventions
+ *  - Plain C: opaque handles, plain pointers and sizes; no exceptions or
+ *    panics cross this boundary.  Every int-returning call returns LGH_OK (0)
+ *    or a negative LGH_ERR_* code; lgh_last_error() then holds a message.
+ *    The reference panics on contract violations (assert!); here the same
+ *    conditions return LGH_ERR_SHAPE and write nothing.
+ *  - Weight blocks are llm-quant's BlockQ4 (18 bytes: LE f16 scale + 16 bytes
+ *    of two's-complement nibbles, element i in the low nibble of qs[i/2] when
+ *    i is even) and BlockQ8_0 (34 bytes: LE f16 scale + 32 int8), row-major
+ *    [n][k/32], consumed as-is (crates/llm-quant/src/lib.rs:17-21, 54-58).
+ *  - Host-pointer calls take and return host memory and are synchronous
+ *    (slice semantics of llm-cpu).  *_dev calls take device pointers, are
+ *    enqueued on the context stream and return before the work completes.
+ *  - One context is used by one thread at a time (llm-cpu's with_threads
+ *    session lock, crates/llm-cpu/src/pool.rs:278-299).
+ *  - n == 0 or m == 0 is a successful no-op, as in the reference
+ *    (crates/llm-cpu/src/gemv_q4.rs:369-371, 698-700).
+ */
+#ifndef LLM_GPU_HIP_H
+#define LLM_GPU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LGH_OK 0
+#define LGH_ERR_INVALID_ARG (-1) /* null handle/pointer or unknown enum value  */
+#define LGH_ERR_SHAPE (-2)       /* k % 32 != 0, mismatched shapes             */
+#define LGH_ERR_HIP (-3)         /* HIP runtime error (message has details)    */
+#define LGH_ERR_ARCH (-4)        /* device is not gfx950                       */
+#define LGH_ERR_NO_DEVICE (-5)   /* no such HIP device                         */
+#define LGH_ERR_OOM (-6)         /* device or host allocation failed           */
+
+/* Accumulation mode, crates/llm-cpu/src/gemv_q4.rs:445-449 AccMode. */
+#define LGH_ASSIGN 0  /* out = W x                                  */
+#define LGH_ADD_F64 1 /* out = (float)((double)out + (double)(W x)) */
+
+/* Activation quantization, crates/llm-cpu/src/gemv_q4.rs:263-271 ActQuant. */
+#define LGH_ACT_PER_BLOCK 0 /* one scale per 32-element block (default) */
+#define LGH_ACT_PER_ROW 1   /* one scale per row, replicated per block  */
+
+#define LGH_BLOCK 32
+#define LGH_BLOCK_Q4_BYTES 18
+#define LGH_BLOCK_Q8_BYTES 34
+
+typedef struct lgh_ctx lgh_ctx; /* device, stream, workspaces, act-quant mode */
+typedef struct lgh_q4 lgh_q4;   /* device-resident Q4 matrix [n, k]           */
+typedef struct lgh_q8 lgh_q8;   /* device-resident Q8_0 matrix [n, k]         */
+
+/* Version string; static, never freed.  Style of llmhost_version(),
+ * crates/llm-capi/src/lib.rs:12-15. */
+const char *lgh_version(void);
+
+/* Open a context on HIP device `device`.  Fails with LGH_ERR_ARCH unless the
+ * device is gfx950.  Replaces CpuBackend::new (crates/llm-cpu/src/lib.rs:46-57)
+ * as the thing a session is bound to. */
+int lgh_init(int device, lgh_ctx **out);
+void lgh_destroy(lgh_ctx *ctx);
+/* Message of the last failed call on ctx (or of the last failed lgh_init when
+ * ctx is NULL).  Valid until the next call on ctx. */
+const char *lgh_last_error(const lgh_ctx *ctx);
+
+/* set_act_quant / current_act_quant (crates/llm-cpu/src/gemv_q4.rs:276-292),
+ * per context instead of process-wide.  Affects the Q4 GEMV/GEMM; the Q8_0
+ * GEMV always quantizes per block (crates/llm-engine/src/weights.rs:197). */
+int lgh_set_act_quant(lgh_ctx *ctx, int mode);
+int lgh_get_act_quant(const lgh_ctx *ctx);
+
+/* Stream used by every call on ctx (a hipStream_t; NULL = the context's own
+ * stream).  Lets a caller enqueue on a stream it already times or orders. */
+int lgh_set_stream(lgh_ctx *ctx, void *hip_stream);
+void *lgh_get_stream(const lgh_ctx *ctx);
+/* Wait for all work enqueued on the context stream. */
+int lgh_sync(lgh_ctx *ctx);
+
+/* ---- weights ------------------------------------------------------------
+ * Q4Matrix::from_blocks (crates/llm-cpu/src/gemv_q4.rs:128-149): upload
+ * row-major BlockQ4[n][k/32] from host memory and repack on the device.
+ * Weights are immutable afterwards. */
+int lgh_q4_upload(lgh_ctx *ctx, const void *blocks, size_t n, size_t k, lgh_q4 **out);
+/* Same, from device-resident BlockQ4 bytes (n*k/32*18 bytes, any alignment). */
+int lgh_q4_upload_dev(lgh_ctx *ctx, const void *blocks_dev, size_t n, size_t k, lgh_q4 **out);
+/* Q4Matrix::from_f32 / Linear::from_f32(.., WeightFormat::Q4_32)
+ * (gemv_q4.rs:116-124, crates/llm-engine/src/weights.rs:36-43): quantize a
+ * row-major fp32 [n, k] host matrix with BlockQ4::quantize
+ * (crates/llm-quant/src/lib.rs:63-79) on the device. */
+int lgh_q4_from_f32(lgh_ctx *ctx, const float *w, size_t n, size_t k, lgh_q4 **out);
+/* Copy the device matrix back as BlockQ4[n][k/32] (18-byte blocks). */
+int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks);
+void lgh_q4_free(lgh_q4 *w);
+size_t lgh_q4_rows(const lgh_q4 *w);
+size_t lgh_q4_cols(const lgh_q4 *w);
+
+/* Q8Matrix (crates/llm-engine/src/weights.rs:126-153): BlockQ8_0[n][k/32]. */
+int lgh_q8_upload(lgh_ctx *ctx, const void *blocks, size_t n, size_t k, lgh_q8 **out);
+/* Q8Matrix::from_f32 with BlockQ8_0::quantize (crates/llm-quant/src/lib.rs:26-37). */
+int lgh_q8_from_f32(lgh_ctx *ctx, const float *w, size_t n, size_t k, lgh_q8 **out);
+int lgh_q8_download(lgh_ctx *ctx, const lgh_q8 *w, void *blocks);
+void lgh_q8_free(lgh_q8 *w);
+size_t lgh_q8_rows(const lgh_q8 *w);
+size_t lgh_q8_cols(const lgh_q8 *w);
+
+/* ---- Q4 GEMV, M = 1 -------------------------------------------------------
+ * gemv_q4 / gemv_q4_add (crates/llm-cpu/src/gemv_q4.rs:344-363):
+ * y[n] = W[n,k] @ x[k] with x quantized per ActQ8 (gemv_q4.rs:62-95); mode
+ * LGH_ADD_F64 adds onto y in f64 (gemv_q4.rs:486-497). */
+int lgh_q4_gemv(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, int mode);
+int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, int mode);
+
+/* gemv_q4_pair (crates/llm-cpu/src/gemv_q4.rs:396-443): SwiGLU gate and up
+ * projections sharing one activation quantization, one launch.  Requires
+ * equal k and equal n (gemv_q4.rs:403-417). */
+int lgh_q4_gemv_pair(lgh_ctx *ctx, const lgh_q4 *w_gate, const lgh_q4 *w_up, const float *x,
+                     float *y_gate, float *y_up);
+int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *w_gate, const lgh_q4 *w_up,
+                         const float *x_dev, float *yg_dev, float *yu_dev);
+
+/* ---- Q4 GEMM, M >= 1 ------------------------------------------------------
+ * gemm_q4 / gemm_q4_add (crates/llm-cpu/src/gemv_q4.rs:686-722):
+ * y[m, n] = x[m, k] @ W[n, k]^T, activations quantized per token with
+ * quantize_batch (gemv_q4.rs:747-798).  m == 1 runs the GEMV. */
+int lgh_q4_gemm(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, size_t m, int mode);
+int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m,
+                    int mode);
+
+/* ---- Q8_0 GEMV ------------------------------------------------------------
+ * q8_apply (crates/llm-engine/src/weights.rs:194-227), reached through
+ * OutputHead::apply (weights.rs:186-192): per token, y[n] = W[n,k] @ x[k]
+ * with per-block ActQ8 activations.  Assign mode only, as in the reference. */
+int lgh_q8_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *x, float *y, size_t tokens);
+int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev,
+                    size_t tokens);
+
+/* ---- test hooks (host pointers, synchronous) -------------------------------
+ * ActQ8::quantize / quantize_row / quantize_batch (gemv_q4.rs:33-95,
+ * 747-798) run by the same device code the GEMV/GEMM use, honouring the
+ * context's act-quant mode: x[m,k] -> qs[m,k], scales[m,k/32], sums[m,k/32]. */
+int lgh_act_quant(lgh_ctx *ctx, const float *x, size_t m, size_t k, int8_t *qs, float *scales,
+                  int32_t *sums);
+/* dot_q4_q8_scalar (gemv_q4.rs:959-966) for nblocks BlockQ4 against a[nblocks*32]
+ * int8, using the GEMV's device unpack + dot instructions; bit-exact target. */
+int lgh_q4_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks,
+                      int32_t *out);
+/* Integer Q8_0 x Q8 block dot (crates/llm-engine/src/weights.rs:206-209). */
+int lgh_q8_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks,
+                      int32_t *out);
+/* Per-block integer dots of the GEMM's int8 MFMA path: out[m, n, k/32] =
+ * sum over block kb of nibble(W[n]) * qs[m] (qs int8 [m, k]); checks the MFMA
+ * operand layout bit-exactly against dot_q4_q8_scalar. */
+int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size_t m,
+                           int32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,562 @@
+// C ABI of libllm_gpu_hip.so: contexts, weight upload/repack, and the GEMV /
+// GEMM / Q8 entry points that stand in for llm-cpu's public functions
+// (crates/llm-cpu/src/lib.rs:21-24) behind llm-engine's Linear / OutputHead
+// seam (crates/llm-engine/src/weights.rs:75-192).
+//
+// Error behaviour: the reference panics on contract violations (assert_eq!
+// on lengths, k % 32); here every such case returns LGH_ERR_SHAPE (or
+// LGH_ERR_INVALID_ARG for null/misaligned pointers) before any work is
+// enqueued, and lgh_last_error() names the violated condition.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+#include "lgh_internal.h"
+
+namespace {
+
+thread_local std::string g_init_err;
+
+int fail(lgh_ctx *ctx, int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx)
+    ctx->err = buf;
+  else
+    g_init_err = buf;
+  return code;
+}
+
+int hip_fail(lgh_ctx *ctx, hipError_t e, const char *what) {
+  return fail(ctx, LGH_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
+}
+
+#define LGH_HIP(ctx, call)                              \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+int set_device(lgh_ctx *ctx) {
+  LGH_HIP(ctx, hipSetDevice(ctx->device));
+  return LGH_OK;
+}
+
+// Grow-only device buffer; waits for queued work before releasing the old one.
+int ensure(lgh_ctx *ctx, void **buf, size_t *cap, size_t bytes) {
+  if (bytes <= *cap) return LGH_OK;
+  if (*buf) {
+    LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    LGH_HIP(ctx, hipFree(*buf));
+    *buf = nullptr;
+    *cap = 0;
+  }
+  const size_t want = align_up(bytes);
+  hipError_t e = hipMalloc(buf, want);
+  if (e != hipSuccess) {
+    *buf = nullptr;
+    return fail(ctx, LGH_ERR_OOM, "hipMalloc(%zu bytes) failed: %s", want, hipGetErrorString(e));
+  }
+  *cap = want;
+  return LGH_OK;
+}
+
+// Carve consecutive 256-byte aligned regions out of the staging buffer.
+struct Carve {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes);
+    return o;
+  }
+};
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Largest K the fused GEMV keeps in LDS (32 B + 4 B per block, 64 KiB);
+// longer rows run through the batched act-quant + GEMM path with m = 1.
+constexpr size_t kGemvMaxBpr = (65536 - 64) / 36;
+
+template <class M>
+int alloc_matrix(lgh_ctx *ctx, size_t n, size_t k, size_t qs_bytes_per_block, M **out) {
+  auto *w = new (std::nothrow) M();
+  if (!w) return fail(ctx, LGH_ERR_OOM, "host allocation failed");
+  w->device = ctx->device;
+  w->n = n;
+  w->k = k;
+  w->bpr = k / 32;
+  const size_t nb = n * w->bpr;
+  const size_t qs_bytes = align_up(nb * qs_bytes_per_block);
+  const size_t bytes = qs_bytes + align_up(nb * 2);
+  void *p = nullptr;
+  if (bytes) {
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+      delete w;
+      return fail(ctx, LGH_ERR_OOM, "hipMalloc(%zu bytes) for weights failed: %s", bytes,
+                  hipGetErrorString(e));
+    }
+  }
+  w->qs = reinterpret_cast<decltype(w->qs)>(p);
+  w->sc = reinterpret_cast<uint16_t *>(static_cast<char *>(p) + qs_bytes);
+  *out = w;
+  return LGH_OK;
+}
+
+template <class M>
+void free_matrix(M *w) {
+  if (!w) return;
+  if (w->qs) {
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(w->device);
+    (void)hipFree(w->qs);
+    (void)hipSetDevice(cur);
+  }
+  delete w;
+}
+
+int check_shape(lgh_ctx *ctx, const void *p, size_t n, size_t k, void *out) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!out) return fail(ctx, LGH_ERR_INVALID_ARG, "null output handle");
+  if (k % 32) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is not a multiple of 32", k);
+  if (n * k && !p) return fail(ctx, LGH_ERR_INVALID_ARG, "null weight pointer");
+  return LGH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *lgh_version(void) { return "llm_gpu_hip 0.1.0 (gfx950, wave64)"; }
+
+int lgh_init(int device, lgh_ctx **out) {
+  if (!out) return fail(nullptr, LGH_ERR_INVALID_ARG, "null ctx out-pointer");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(nullptr, LGH_ERR_NO_DEVICE, "no HIP device (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= count)
+    return fail(nullptr, LGH_ERR_NO_DEVICE, "device %d out of range (count %d)", device, count);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(nullptr, LGH_ERR_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, LGH_ERR_ARCH, "device %d is %s, this library is built for gfx950 only", device,
+                prop.gcnArchName);
+  auto *ctx = new (std::nothrow) lgh_ctx();
+  if (!ctx) return fail(nullptr, LGH_ERR_OOM, "host allocation failed");
+  ctx->device = device;
+  ctx->cu_count = prop.multiProcessorCount;
+  e = hipSetDevice(device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return fail(nullptr, LGH_ERR_HIP, "stream creation failed: %s", hipGetErrorString(e));
+  }
+  ctx->stream = ctx->own_stream;
+  *out = ctx;
+  return LGH_OK;
+}
+
+void lgh_destroy(lgh_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->stage) (void)hipFree(ctx->stage);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  delete ctx;
+}
+
+const char *lgh_last_error(const lgh_ctx *ctx) { return ctx ? ctx->err.c_str() : g_init_err.c_str(); }
+
+int lgh_set_act_quant(lgh_ctx *ctx, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (mode != LGH_ACT_PER_BLOCK && mode != LGH_ACT_PER_ROW)
+    return fail(ctx, LGH_ERR_INVALID_ARG, "unknown act-quant mode %d", mode);
+  ctx->act_mode = mode;
+  return LGH_OK;
+}
+
+int lgh_get_act_quant(const lgh_ctx *ctx) { return ctx ? ctx->act_mode : LGH_ERR_INVALID_ARG; }
+
+int lgh_set_stream(lgh_ctx *ctx, void *hip_stream) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (int r = set_device(ctx)) return r;
+  // Work already queued may still read the workspaces: finish it first.
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+  return LGH_OK;
+}
+
+void *lgh_get_stream(const lgh_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
+
+int lgh_sync(lgh_ctx *ctx) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+// ---- weights -------------------------------------------------------------
+int lgh_q4_upload_dev(lgh_ctx *ctx, const void *blocks_dev, size_t n, size_t k, lgh_q4 **out) {
+  if (int r = check_shape(ctx, blocks_dev, n, k, out)) return r;
+  if (int r = set_device(ctx)) return r;
+  lgh_q4 *w = nullptr;
+  if (int r = alloc_matrix(ctx, n, k, 16, &w)) return r;
+  hipError_t e = lgh::launch_q4_repack(static_cast<const uint8_t *>(blocks_dev), n * w->bpr, w->qs, w->sc,
+                                       ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_matrix(w);
+    return hip_fail(ctx, e, "Q4 repack");
+  }
+  *out = w;
+  return LGH_OK;
+}
+
+int lgh_q4_upload(lgh_ctx *ctx, const void *blocks, size_t n, size_t k, lgh_q4 **out) {
+  if (int r = check_shape(ctx, blocks, n, k, out)) return r;
+  if (int r = set_device(ctx)) return r;
+  const size_t bytes = n * (k / 32) * LGH_BLOCK_Q4_BYTES;
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, bytes)) return r;
+  if (bytes) LGH_HIP(ctx, hipMemcpyAsync(ctx->stage, blocks, bytes, hipMemcpyHostToDevice, ctx->stream));
+  return lgh_q4_upload_dev(ctx, ctx->stage, n, k, out);
+}
+
+int lgh_q4_from_f32(lgh_ctx *ctx, const float *wf, size_t n, size_t k, lgh_q4 **out) {
+  if (int r = check_shape(ctx, wf, n, k, out)) return r;
+  if (int r = set_device(ctx)) return r;
+  const size_t bytes = n * k * sizeof(float);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, bytes)) return r;
+  lgh_q4 *w = nullptr;
+  if (int r = alloc_matrix(ctx, n, k, 16, &w)) return r;
+  hipError_t e = bytes ? hipMemcpyAsync(ctx->stage, wf, bytes, hipMemcpyHostToDevice, ctx->stream) : hipSuccess;
+  if (e == hipSuccess)
+    e = lgh::launch_q4_quantize(static_cast<const float *>(ctx->stage), n * w->bpr, w->qs, w->sc, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_matrix(w);
+    return hip_fail(ctx, e, "Q4 quantize");
+  }
+  *out = w;
+  return LGH_OK;
+}
+
+int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w || !blocks) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = set_device(ctx)) return r;
+  const size_t nb = w->n * w->bpr, bytes = nb * LGH_BLOCK_Q4_BYTES;
+  if (!bytes) return LGH_OK;
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, bytes)) return r;
+  LGH_HIP(ctx, lgh::launch_q4_unpack(w->qs, w->sc, nb, static_cast<uint8_t *>(ctx->stage), ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(blocks, ctx->stage, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+void lgh_q4_free(lgh_q4 *w) { free_matrix(w); }
+size_t lgh_q4_rows(const lgh_q4 *w) { return w ? w->n : 0; }
+size_t lgh_q4_cols(const lgh_q4 *w) { return w ? w->k : 0; }
+
+int lgh_q8_upload(lgh_ctx *ctx, const void *blocks, size_t n, size_t k, lgh_q8 **out) {
+  if (int r = check_shape(ctx, blocks, n, k, out)) return r;
+  if (int r = set_device(ctx)) return r;
+  const size_t nb = n * (k / 32), bytes = nb * LGH_BLOCK_Q8_BYTES;
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, bytes)) return r;
+  lgh_q8 *w = nullptr;
+  if (int r = alloc_matrix(ctx, n, k, 32, &w)) return r;
+  hipError_t e = bytes ? hipMemcpyAsync(ctx->stage, blocks, bytes, hipMemcpyHostToDevice, ctx->stream) : hipSuccess;
+  if (e == hipSuccess)
+    e = lgh::launch_q8_repack(static_cast<const uint8_t *>(ctx->stage), nb, w->qs, w->sc, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_matrix(w);
+    return hip_fail(ctx, e, "Q8 upload");
+  }
+  *out = w;
+  return LGH_OK;
+}
+
+int lgh_q8_from_f32(lgh_ctx *ctx, const float *wf, size_t n, size_t k, lgh_q8 **out) {
+  if (int r = check_shape(ctx, wf, n, k, out)) return r;
+  if (int r = set_device(ctx)) return r;
+  const size_t bytes = n * k * sizeof(float);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, bytes)) return r;
+  lgh_q8 *w = nullptr;
+  if (int r = alloc_matrix(ctx, n, k, 32, &w)) return r;
+  hipError_t e = bytes ? hipMemcpyAsync(ctx->stage, wf, bytes, hipMemcpyHostToDevice, ctx->stream) : hipSuccess;
+  if (e == hipSuccess)
+    e = lgh::launch_q8_quantize(static_cast<const float *>(ctx->stage), n * w->bpr, w->qs, w->sc, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_matrix(w);
+    return hip_fail(ctx, e, "Q8 quantize");
+  }
+  *out = w;
+  return LGH_OK;
+}
+
+int lgh_q8_download(lgh_ctx *ctx, const lgh_q8 *w, void *blocks) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w || !blocks) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = set_device(ctx)) return r;
+  const size_t nb = w->n * w->bpr, bytes = nb * LGH_BLOCK_Q8_BYTES;
+  if (!bytes) return LGH_OK;
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, bytes)) return r;
+  LGH_HIP(ctx, lgh::launch_q8_unpack(w->qs, w->sc, nb, static_cast<uint8_t *>(ctx->stage), ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(blocks, ctx->stage, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+void lgh_q8_free(lgh_q8 *w) { free_matrix(w); }
+size_t lgh_q8_rows(const lgh_q8 *w) { return w ? w->n : 0; }
+size_t lgh_q8_cols(const lgh_q8 *w) { return w ? w->k : 0; }
+
+// ---- device-pointer entry points -------------------------------------------
+static int check_mode(lgh_ctx *ctx, int mode) {
+  if (mode != LGH_ASSIGN && mode != LGH_ADD_F64)
+    return fail(ctx, LGH_ERR_INVALID_ARG, "unknown accumulation mode %d", mode);
+  return LGH_OK;
+}
+
+int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode);
+
+int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  if (w->bpr > kGemvMaxBpr) return lgh_q4_gemm_dev(ctx, w, x_dev, y_dev, 1, mode);
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_q4_gemv(w, y_dev, nullptr, nullptr, x_dev, mode, ctx->act_mode, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const float *x_dev, float *yg_dev,
+                         float *yu_dev) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!wg || !wu) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (wg->k != wu->k || wg->n != wu->n)
+    return fail(ctx, LGH_ERR_SHAPE, "pair needs equal shapes: gate %zux%zu, up %zux%zu", wg->n, wg->k, wu->n,
+                wu->k);
+  if (wg->n == 0) return LGH_OK;
+  if (!yg_dev || !yu_dev || (wg->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  if (wg->bpr > kGemvMaxBpr) {
+    if (int r = lgh_q4_gemm_dev(ctx, wg, x_dev, yg_dev, 1, LGH_ASSIGN)) return r;
+    return lgh_q4_gemm_dev(ctx, wu, x_dev, yu_dev, 1, LGH_ASSIGN);
+  }
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_q4_gemv(wg, yg_dev, wu, yu_dev, x_dev, LGH_ASSIGN, ctx->act_mode, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (m == 0 || w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  if (m == 1 && w->bpr <= kGemvMaxBpr) return lgh_q4_gemv_dev(ctx, w, x_dev, y_dev, mode);
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t o_qs = cv.take(m * w->k);
+  const size_t o_sa = cv.take(m * w->bpr * sizeof(float));
+  const size_t o_rs = cv.take(m * sizeof(float));
+  if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
+  char *ws = static_cast<char *>(ctx->ws);
+  auto *qs = reinterpret_cast<int8_t *>(ws + o_qs);
+  auto *sa = reinterpret_cast<float *>(ws + o_sa);
+  auto *rs = reinterpret_cast<float *>(ws + o_rs);
+  LGH_HIP(ctx, lgh::launch_act_quant(x_dev, m, w->k, ctx->act_mode, qs, sa, nullptr, rs, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q4_gemm(w, qs, sa, y_dev, m, mode, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev, size_t tokens) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (tokens == 0 || w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  if (w->bpr > kGemvMaxBpr) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", kGemvMaxBpr * 32);
+  if (tokens > 65535) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports at most 65535 tokens per call");
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_q8_gemv(w, x_dev, y_dev, tokens, ctx->stream));
+  return LGH_OK;
+}
+
+// ---- host-pointer entry points ----------------------------------------------
+int lgh_q4_gemv(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, int mode) {
+  return lgh_q4_gemm(ctx, w, x, y, 1, mode);
+}
+
+int lgh_q4_gemm(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, size_t m, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (m == 0 || w->n == 0) return LGH_OK;
+  if (!x || !y) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = m * w->k * sizeof(float), yb = m * w->n * sizeof(float);
+  const size_t ox = cv.take(xb), oy = cv.take(yb);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *yd = reinterpret_cast<float *>(st + oy);
+  LGH_HIP(ctx, hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (mode == LGH_ADD_F64) LGH_HIP(ctx, hipMemcpyAsync(yd, y, yb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q4_gemm_dev(ctx, w, xd, yd, m, mode)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_gemv_pair(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const float *x, float *y_gate,
+                     float *y_up) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!wg || !wu) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (wg->k != wu->k || wg->n != wu->n)
+    return fail(ctx, LGH_ERR_SHAPE, "pair needs equal shapes: gate %zux%zu, up %zux%zu", wg->n, wg->k, wu->n,
+                wu->k);
+  if (wg->n == 0) return LGH_OK;
+  if (!x || !y_gate || !y_up) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = wg->k * sizeof(float), yb = wg->n * sizeof(float);
+  const size_t ox = cv.take(xb), og = cv.take(yb), ou = cv.take(yb);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox);
+  float *gd = reinterpret_cast<float *>(st + og), *ud = reinterpret_cast<float *>(st + ou);
+  LGH_HIP(ctx, hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q4_gemv_pair_dev(ctx, wg, wu, xd, gd, ud)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(y_gate, gd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(y_up, ud, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q8_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *x, float *y, size_t tokens) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (tokens == 0 || w->n == 0) return LGH_OK;
+  if (!x || !y) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = tokens * w->k * sizeof(float), yb = tokens * w->n * sizeof(float);
+  const size_t ox = cv.take(xb), oy = cv.take(yb);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *yd = reinterpret_cast<float *>(st + oy);
+  LGH_HIP(ctx, hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q8_gemv_dev(ctx, w, xd, yd, tokens)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+// ---- test hooks ---------------------------------------------------------------
+int lgh_act_quant(lgh_ctx *ctx, const float *x, size_t m, size_t k, int8_t *qs, float *scales, int32_t *sums) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (k % 32) return fail(ctx, LGH_ERR_SHAPE, "activation length %zu is not a multiple of 32", k);
+  if (m == 0 || k == 0) return LGH_OK;
+  if (!x || !qs || !scales) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = set_device(ctx)) return r;
+  const size_t bpr = k / 32;
+  Carve cv;
+  const size_t ox = cv.take(m * k * 4), oq = cv.take(m * k), os = cv.take(m * bpr * 4), ou = cv.take(m * bpr * 4),
+               orow = cv.take(m * 4);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  LGH_HIP(ctx, hipMemcpyAsync(st + ox, x, m * k * 4, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_act_quant(reinterpret_cast<float *>(st + ox), m, k, ctx->act_mode,
+                                     reinterpret_cast<int8_t *>(st + oq), reinterpret_cast<float *>(st + os),
+                                     reinterpret_cast<int32_t *>(st + ou), reinterpret_cast<float *>(st + orow),
+                                     ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(qs, st + oq, m * k, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(scales, st + os, m * bpr * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (sums) LGH_HIP(ctx, hipMemcpyAsync(sums, st + ou, m * bpr * 4, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks, int32_t *out) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (nblocks == 0) return LGH_OK;
+  if (!blocks || !a || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t oraw = cv.take(nblocks * 18), oqs = cv.take(nblocks * 16), osc = cv.take(nblocks * 2),
+               oa = cv.take(nblocks * 32), oo = cv.take(nblocks * 4);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  LGH_HIP(ctx, hipMemcpyAsync(st + oraw, blocks, nblocks * 18, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(st + oa, a, nblocks * 32, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q4_repack(reinterpret_cast<uint8_t *>(st + oraw), nblocks,
+                                     reinterpret_cast<uint8_t *>(st + oqs), reinterpret_cast<uint16_t *>(st + osc),
+                                     ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q4_block_dots(reinterpret_cast<uint8_t *>(st + oqs), reinterpret_cast<int8_t *>(st + oa),
+                                         nblocks, reinterpret_cast<int32_t *>(st + oo), ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(out, st + oo, nblocks * 4, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q8_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks, int32_t *out) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (nblocks == 0) return LGH_OK;
+  if (!blocks || !a || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t oraw = cv.take(nblocks * 34), oqs = cv.take(nblocks * 32), osc = cv.take(nblocks * 2),
+               oa = cv.take(nblocks * 32), oo = cv.take(nblocks * 4);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  LGH_HIP(ctx, hipMemcpyAsync(st + oraw, blocks, nblocks * 34, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(st + oa, a, nblocks * 32, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q8_repack(reinterpret_cast<uint8_t *>(st + oraw), nblocks,
+                                     reinterpret_cast<int8_t *>(st + oqs), reinterpret_cast<uint16_t *>(st + osc),
+                                     ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q8_block_dots(reinterpret_cast<int8_t *>(st + oqs), reinterpret_cast<int8_t *>(st + oa),
+                                         nblocks, reinterpret_cast<int32_t *>(st + oo), ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(out, st + oo, nblocks * 4, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size_t m, int32_t *out) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (m == 0 || w->n == 0 || w->bpr == 0) return LGH_OK;
+  if (!qs || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = set_device(ctx)) return r;
+  const size_t ob_bytes = m * w->n * w->bpr * 4;
+  Carve cv;
+  const size_t oq = cv.take(m * w->k), oo = cv.take(ob_bytes);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  LGH_HIP(ctx, hipMemcpyAsync(st + oq, qs, m * w->k, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q4_mfma_block_dots(w, reinterpret_cast<int8_t *>(st + oq), m,
+                                              reinterpret_cast<int32_t *>(st + oo), ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(out, st + oo, ob_bytes, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+}  // extern "C"

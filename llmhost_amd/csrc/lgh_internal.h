@@ -1,0 +1,96 @@
+// Internal declarations shared by the HIP sources of libllm_gpu_hip.so.
+//
+// Device layout of a Q4 matrix (built once at upload, immutable after):
+//   qs plane: uint8 [n][bpr][16]  -- the 16 nibble bytes of each BlockQ4,
+//             re-paired so that dword d (d = 0..3) of a block holds elements
+//             8d..8d+3 in its low nibbles and 8d+4..8d+7 in its high nibbles
+//             (still two's-complement nibbles, no offset);
+//   sc plane: uint16 [n][bpr]     -- the block's f16 scale bits, unchanged.
+// 16 + 2 = 18 bytes per 32 weights, exactly the BlockQ4 footprint, but every
+// block's nibbles are 16-byte aligned so a lane moves a block with one
+// 128-bit load.  Unpacking dword d: (d << 4) & 0xF0F0F0F0 yields elements
+// 8d..8d+3 and d & 0xF0F0F0F0 yields 8d+4..8d+7, each as a signed int8
+// equal to 16 x the nibble value -- natural element order, no sign fix-up.
+// The factor 16 is exact and is removed once per output (x 1/16).
+//
+// Q8_0 matrix: qs plane int8 [n][bpr][32] (natural order) + sc plane f16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/llm_gpu_hip.h"
+
+struct lgh_ctx {
+  int device = 0;
+  int cu_count = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  int act_mode = LGH_ACT_PER_BLOCK;
+  std::string err;
+  // GEMM activation workspace: int8 qs [m][k] + f32 scales [m][k/32] + f32 row scales [m].
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+  // Device staging for the host-pointer entry points.
+  void *stage = nullptr;
+  size_t stage_bytes = 0;
+};
+
+struct lgh_q4 {
+  int device = 0;
+  size_t n = 0, k = 0, bpr = 0;
+  uint8_t *qs = nullptr;   // n*bpr*16 bytes
+  uint16_t *sc = nullptr;  // n*bpr halves (same allocation as qs)
+};
+
+struct lgh_q8 {
+  int device = 0;
+  size_t n = 0, k = 0, bpr = 0;
+  int8_t *qs = nullptr;    // n*bpr*32 bytes
+  uint16_t *sc = nullptr;
+};
+
+// ---- internal launchers (return hipError_t of the launch) ----------------
+// All enqueue on `stream`; all pointers are device pointers.
+namespace lgh {
+
+hipError_t launch_q4_repack(const uint8_t *raw_blocks, size_t nblocks, uint8_t *qs, uint16_t *sc,
+                            hipStream_t stream);
+hipError_t launch_q4_unpack(const uint8_t *qs, const uint16_t *sc, size_t nblocks, uint8_t *raw,
+                            hipStream_t stream);
+hipError_t launch_q8_repack(const uint8_t *raw_blocks, size_t nblocks, int8_t *qs, uint16_t *sc,
+                            hipStream_t stream);
+hipError_t launch_q8_unpack(const int8_t *qs, const uint16_t *sc, size_t nblocks, uint8_t *raw,
+                            hipStream_t stream);
+hipError_t launch_q4_quantize(const float *w, size_t nblocks, uint8_t *qs, uint16_t *sc,
+                              hipStream_t stream);
+hipError_t launch_q8_quantize(const float *w, size_t nblocks, int8_t *qs, uint16_t *sc,
+                              hipStream_t stream);
+
+// GEMV: y = W x for one or two matrices sharing x (pair).  w1 may be null.
+hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
+                          int mode, int per_row, hipStream_t stream);
+hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens,
+                          hipStream_t stream);
+
+// Batched activation quantization: x[m][k] -> qs[m][k], scales[m][k/32]
+// (+ sums if non-null).  row_scale: scratch of m floats (used for per_row).
+hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int8_t *qs,
+                            float *scales, int32_t *sums, float *row_scale, hipStream_t stream);
+
+// GEMM on pre-quantized activations: y[m][n] (+)= aq[m][k] . W^T.
+hipError_t launch_q4_gemm(const lgh_q4 *w, const int8_t *aq, const float *sa, float *y, size_t m,
+                          int mode, hipStream_t stream);
+
+// Test hooks.
+hipError_t launch_q4_block_dots(const uint8_t *qs, const int8_t *a, size_t nblocks, int32_t *out,
+                                hipStream_t stream);
+hipError_t launch_q8_block_dots(const int8_t *qs, const int8_t *a, size_t nblocks, int32_t *out,
+                                hipStream_t stream);
+hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const int8_t *aq, size_t m, int32_t *out,
+                                     hipStream_t stream);
+
+}  // namespace lgh

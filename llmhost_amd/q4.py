@@ -1,0 +1,383 @@
+"""Host-side mirror of llm-cpu's quantized-matmul API on the HIP library.
+
+Same names, argument meaning and error behaviour as the reference functions
+(crates/llm-cpu/src/gemv_q4.rs, re-exported at crates/llm-cpu/src/lib.rs:21-24),
+with the computation done by libllm_gpu_hip.so on one MI355X:
+
+    Q4Matrix.from_blocks(n, k, blocks) / Q4Matrix.from_f32(w, n, k)
+    gemv_q4(w, x, out) / gemv_q4_add(w, x, dst) / gemv_q4_pair(wg, wu, x, og, ou)
+    gemm_q4(w, x, out, m) / gemm_q4_add(w, x, out, m)
+    ActQ8.quantize(x) / ActQ8.quantize_row(x)
+    set_act_quant(ActQuant.PerRow) / current_act_quant()
+    Q8Matrix + q8_apply (crates/llm-engine/src/weights.rs:126-227)
+
+Operands are numpy arrays (host memory, synchronous, like the reference's
+slices) or torch tensors on the GPU (device memory, enqueued on the
+context's stream).  Where the reference `assert!`s (length mismatch,
+k % 32 != 0) these raise ``LghShapeError`` (a ValueError) and write nothing.
+
+A process-wide default context (device 0) plays the role of llm-cpu's
+process-wide state; ``Context`` objects can be passed explicitly instead.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import threading
+
+import numpy as np
+
+from . import _ffi
+from ._ffi import LghShapeError, check, lib
+from .formats import BLOCK_Q4, BLOCK_Q8_0, BLOCK_SIZE
+
+
+class ActQuant(enum.IntEnum):
+    """gemv_q4.rs:263-271."""
+
+    PerBlock = _ffi.LGH_ACT_PER_BLOCK
+    PerRow = _ffi.LGH_ACT_PER_ROW
+
+
+class Context:
+    """An lgh_ctx: one device, one stream, workspaces, act-quant mode."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        code = lib().lgh_init(device, C.byref(h))
+        if code != _ffi.LGH_OK:
+            raise _ffi.LghError(code, lib().lgh_last_error(None).decode())
+        self.handle = h
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().lgh_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, code: int) -> None:
+        check(code, self.handle)
+
+    def set_act_quant(self, mode: ActQuant) -> None:
+        self.check(lib().lgh_set_act_quant(self.handle, int(mode)))
+
+    def act_quant(self) -> ActQuant:
+        return ActQuant(lib().lgh_get_act_quant(self.handle))
+
+    def set_stream(self, stream_handle: int | None) -> None:
+        """Use a hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
+        self.check(lib().lgh_set_stream(self.handle, C.c_void_p(stream_handle or 0)))
+
+    def stream(self) -> int:
+        return lib().lgh_get_stream(self.handle) or 0
+
+    def sync(self) -> None:
+        self.check(lib().lgh_sync(self.handle))
+
+
+_default_ctx: Context | None = None
+_default_lock = threading.Lock()
+
+
+def default_context() -> Context:
+    global _default_ctx
+    with _default_lock:
+        if _default_ctx is None:
+            _default_ctx = Context(0)
+        return _default_ctx
+
+
+def set_act_quant(mode: ActQuant, ctx: Context | None = None) -> None:
+    """set_act_quant (gemv_q4.rs:276-282), per context."""
+    (ctx or default_context()).set_act_quant(mode)
+
+
+def current_act_quant(ctx: Context | None = None) -> ActQuant:
+    """current_act_quant (gemv_q4.rs:286-292)."""
+    return (ctx or default_context()).act_quant()
+
+
+# ---- operand plumbing ------------------------------------------------------
+def _is_torch(a) -> bool:
+    return type(a).__module__.startswith("torch")
+
+
+def _host_f32(a, name: str) -> np.ndarray:
+    if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags["C_CONTIGUOUS"]:
+        raise TypeError(f"{name} must be a C-contiguous float32 numpy array")
+    return a
+
+
+def _dev_ptr(a, name: str) -> C.c_void_p:
+    import torch
+
+    if a.device.type != "cuda" or a.dtype != torch.float32 or not a.is_contiguous():
+        raise TypeError(f"{name} must be a contiguous float32 tensor on the GPU")
+    return C.c_void_p(a.data_ptr())
+
+
+def _np_ptr(a: np.ndarray) -> C.c_void_p:
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _shape_assert(cond: bool, msg: str) -> None:
+    if not cond:
+        raise LghShapeError(_ffi.LGH_ERR_SHAPE, msg)
+
+
+# ---- matrices -----------------------------------------------------------------
+class Q4Matrix:
+    """Device-resident Q4 matrix [n, k] (gemv_q4.rs:97-209)."""
+
+    def __init__(self, handle: C.c_void_p, n: int, k: int, ctx: Context):
+        self._h = handle
+        self.n = n
+        self.k = k
+        self.ctx = ctx
+
+    @classmethod
+    def from_blocks(cls, n: int, k: int, blocks: np.ndarray, ctx: Context | None = None) -> "Q4Matrix":
+        """Q4Matrix::from_blocks (gemv_q4.rs:128-149)."""
+        ctx = ctx or default_context()
+        _shape_assert(k % BLOCK_SIZE == 0, f"K={k} is not a multiple of {BLOCK_SIZE}")
+        h = C.c_void_p()
+        if _is_torch(blocks):
+            _shape_assert(blocks.numel() * blocks.element_size() == n * (k // 32) * 18,
+                          "blocks byte length != n*k/32*18")
+            ctx.check(lib().lgh_q4_upload_dev(ctx.handle, C.c_void_p(blocks.data_ptr()), n, k, C.byref(h)))
+        else:
+            blocks = np.ascontiguousarray(blocks)
+            _shape_assert(blocks.dtype == BLOCK_Q4 and blocks.size == n * (k // 32),
+                          f"expected {n * (k // 32)} BlockQ4 blocks")
+            ctx.check(lib().lgh_q4_upload(ctx.handle, _np_ptr(blocks), n, k, C.byref(h)))
+        return cls(h, n, k, ctx)
+
+    @classmethod
+    def from_f32(cls, weight: np.ndarray, n: int, k: int, ctx: Context | None = None) -> "Q4Matrix":
+        """Q4Matrix::from_f32 (gemv_q4.rs:116-124): BlockQ4::quantize on the GPU."""
+        ctx = ctx or default_context()
+        w = _host_f32(np.ascontiguousarray(weight, dtype=np.float32), "weight")
+        _shape_assert(w.size == n * k, f"weight length {w.size} != {n}*{k}")
+        _shape_assert(k % BLOCK_SIZE == 0, f"K={k} is not a multiple of {BLOCK_SIZE}")
+        h = C.c_void_p()
+        ctx.check(lib().lgh_q4_from_f32(ctx.handle, _np_ptr(w), n, k, C.byref(h)))
+        return cls(h, n, k, ctx)
+
+    def blocks(self) -> np.ndarray:
+        """The matrix as row-major BlockQ4[n][k/32] (as uploaded)."""
+        out = np.zeros(self.n * (self.k // 32), dtype=BLOCK_Q4)
+        self.ctx.check(lib().lgh_q4_download(self.ctx.handle, self._h, _np_ptr(out)))
+        return out
+
+    def blocks_per_row(self) -> int:
+        return self.k // BLOCK_SIZE
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            lib().lgh_q4_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Q8Matrix:
+    """Device-resident Q8_0 matrix (crates/llm-engine/src/weights.rs:126-153)."""
+
+    def __init__(self, handle: C.c_void_p, n: int, k: int, ctx: Context):
+        self._h = handle
+        self.n = n
+        self.k = k
+        self.ctx = ctx
+
+    @classmethod
+    def from_blocks(cls, n: int, k: int, blocks: np.ndarray, ctx: Context | None = None) -> "Q8Matrix":
+        ctx = ctx or default_context()
+        _shape_assert(k % BLOCK_SIZE == 0, f"K={k} is not a multiple of {BLOCK_SIZE}")
+        blocks = np.ascontiguousarray(blocks)
+        _shape_assert(blocks.dtype == BLOCK_Q8_0 and blocks.size == n * (k // 32),
+                      f"expected {n * (k // 32)} BlockQ8_0 blocks")
+        h = C.c_void_p()
+        ctx.check(lib().lgh_q8_upload(ctx.handle, _np_ptr(blocks), n, k, C.byref(h)))
+        return cls(h, n, k, ctx)
+
+    @classmethod
+    def from_f32(cls, weight: np.ndarray, n: int, k: int, ctx: Context | None = None) -> "Q8Matrix":
+        """Q8Matrix::from_f32 (weights.rs:133-142): BlockQ8_0::quantize on the GPU."""
+        ctx = ctx or default_context()
+        w = _host_f32(np.ascontiguousarray(weight, dtype=np.float32), "weight")
+        _shape_assert(w.size == n * k, f"weight length {w.size} != {n}*{k}")
+        _shape_assert(k % BLOCK_SIZE == 0, f"K={k} is not a multiple of {BLOCK_SIZE}")
+        h = C.c_void_p()
+        ctx.check(lib().lgh_q8_from_f32(ctx.handle, _np_ptr(w), n, k, C.byref(h)))
+        return cls(h, n, k, ctx)
+
+    def blocks(self) -> np.ndarray:
+        out = np.zeros(self.n * (self.k // 32), dtype=BLOCK_Q8_0)
+        self.ctx.check(lib().lgh_q8_download(self.ctx.handle, self._h, _np_ptr(out)))
+        return out
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            lib().lgh_q8_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---- activation quant ----------------------------------------------------------
+class ActQ8:
+    """ActQ8 (gemv_q4.rs:25-95) computed by the device act-quant kernel."""
+
+    def __init__(self, qs: np.ndarray, scales: np.ndarray, sums: np.ndarray):
+        self.qs = qs
+        self.scales = scales
+        self.sums = sums
+
+    @classmethod
+    def _run(cls, x: np.ndarray, mode: ActQuant, ctx: Context | None) -> "ActQ8":
+        ctx = ctx or default_context()
+        x = _host_f32(np.ascontiguousarray(x, dtype=np.float32), "x")
+        k = x.shape[-1]
+        _shape_assert(k % BLOCK_SIZE == 0, f"activation length {k} is not a multiple of {BLOCK_SIZE}")
+        m = x.size // k if k else 0
+        qs = np.zeros(x.shape, dtype=np.int8)
+        sc = np.zeros(x.shape[:-1] + (k // 32,), dtype=np.float32)
+        su = np.zeros(x.shape[:-1] + (k // 32,), dtype=np.int32)
+        prev = ctx.act_quant()
+        ctx.set_act_quant(mode)
+        try:
+            ctx.check(lib().lgh_act_quant(ctx.handle, _np_ptr(x), m, k, _np_ptr(qs), _np_ptr(sc), _np_ptr(su)))
+        finally:
+            ctx.set_act_quant(prev)
+        return cls(qs, sc, su)
+
+    @classmethod
+    def quantize(cls, x, ctx: Context | None = None) -> "ActQ8":
+        """ActQ8::quantize (gemv_q4.rs:35-40): per-block scales."""
+        return cls._run(x, ActQuant.PerBlock, ctx)
+
+    @classmethod
+    def quantize_row(cls, x, ctx: Context | None = None) -> "ActQ8":
+        """ActQ8::quantize_row (gemv_q4.rs:44-49): one scale per row."""
+        return cls._run(x, ActQuant.PerRow, ctx)
+
+
+# ---- GEMV / GEMM ----------------------------------------------------------------
+def _gemm(w: Q4Matrix, x, out, m: int, mode: int) -> None:
+    ctx = w.ctx
+    if _is_torch(x) or _is_torch(out):
+        _shape_assert(x.numel() == m * w.k, f"x length {x.numel()} != {m}*{w.k}")
+        _shape_assert(out.numel() == m * w.n, f"out length {out.numel()} != {m}*{w.n}")
+        ctx.check(lib().lgh_q4_gemm_dev(ctx.handle, w.handle, _dev_ptr(x, "x"), _dev_ptr(out, "out"), m, mode))
+        return
+    x = _host_f32(x, "x")
+    out = _host_f32(out, "out")
+    _shape_assert(x.size == m * w.k, f"x length {x.size} != {m}*{w.k}")
+    _shape_assert(out.size == m * w.n, f"out length {out.size} != {m}*{w.n}")
+    ctx.check(lib().lgh_q4_gemm(ctx.handle, w.handle, _np_ptr(x), _np_ptr(out), m, mode))
+
+
+def gemv_q4(w: Q4Matrix, x, out) -> None:
+    """`out[n] = W[n, k] @ x[k]` with on-the-fly Q8 activations (gemv_q4.rs:344-352)."""
+    _gemm(w, x, out, 1, _ffi.LGH_ASSIGN)
+
+
+def gemv_q4_add(w: Q4Matrix, x, dst) -> None:
+    """Adds the product onto dst in f64 (gemv_q4.rs:355-363)."""
+    _gemm(w, x, dst, 1, _ffi.LGH_ADD_F64)
+
+
+def gemm_q4(w: Q4Matrix, x, out, m: int) -> None:
+    """Prefill `out[m, n] = X[m, k] @ W[n, k]^T` (gemv_q4.rs:686-688)."""
+    _gemm(w, x, out, m, _ffi.LGH_ASSIGN)
+
+
+def gemm_q4_add(w: Q4Matrix, x, out, m: int) -> None:
+    """Like gemm_q4 but adds onto out in f64 (gemv_q4.rs:691-693)."""
+    _gemm(w, x, out, m, _ffi.LGH_ADD_F64)
+
+
+def gemv_q4_pair(w_gate: Q4Matrix, w_up: Q4Matrix, x, out_gate, out_up) -> None:
+    """Gate and up GEMVs sharing one activation quant (gemv_q4.rs:396-443)."""
+    ctx = w_gate.ctx
+    _shape_assert(w_gate.k == w_up.k, "gate/up K differ")
+    _shape_assert(w_gate.n == w_up.n, "gate/up N differ")
+    if _is_torch(x):
+        _shape_assert(x.numel() == w_gate.k, "x length != K")
+        _shape_assert(out_gate.numel() == w_gate.n and out_up.numel() == w_up.n, "out length != N")
+        ctx.check(lib().lgh_q4_gemv_pair_dev(ctx.handle, w_gate.handle, w_up.handle, _dev_ptr(x, "x"),
+                                             _dev_ptr(out_gate, "out_gate"), _dev_ptr(out_up, "out_up")))
+        return
+    x = _host_f32(x, "x")
+    out_gate = _host_f32(out_gate, "out_gate")
+    out_up = _host_f32(out_up, "out_up")
+    _shape_assert(x.size == w_gate.k, "x length != K")
+    _shape_assert(out_gate.size == w_gate.n and out_up.size == w_up.n, "out length != N")
+    ctx.check(lib().lgh_q4_gemv_pair(ctx.handle, w_gate.handle, w_up.handle, _np_ptr(x), _np_ptr(out_gate),
+                                     _np_ptr(out_up)))
+
+
+def q8_apply(m: Q8Matrix, x, tokens: int, out) -> None:
+    """q8_apply (crates/llm-engine/src/weights.rs:194-227)."""
+    ctx = m.ctx
+    if _is_torch(x):
+        _shape_assert(x.numel() == tokens * m.k and out.numel() == tokens * m.n, "length mismatch")
+        ctx.check(lib().lgh_q8_gemv_dev(ctx.handle, m.handle, _dev_ptr(x, "x"), _dev_ptr(out, "out"), tokens))
+        return
+    x = _host_f32(x, "x")
+    out = _host_f32(out, "out")
+    _shape_assert(x.size == tokens * m.k and out.size == tokens * m.n, "length mismatch")
+    ctx.check(lib().lgh_q8_gemv(ctx.handle, m.handle, _np_ptr(x), _np_ptr(out), tokens))
+
+
+# ---- test hooks ---------------------------------------------------------------------
+def q4_block_dots(blocks: np.ndarray, a: np.ndarray, ctx: Context | None = None) -> np.ndarray:
+    """Device per-block dots nibble(W) . a (dot_q4_q8_scalar, gemv_q4.rs:959-966)."""
+    ctx = ctx or default_context()
+    blocks = np.ascontiguousarray(blocks.ravel())
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    assert blocks.dtype == BLOCK_Q4 and a.size == blocks.size * 32
+    out = np.zeros(blocks.size, dtype=np.int32)
+    ctx.check(lib().lgh_q4_block_dots(ctx.handle, _np_ptr(blocks), _np_ptr(a), blocks.size, _np_ptr(out)))
+    return out
+
+
+def q8_block_dots(blocks: np.ndarray, a: np.ndarray, ctx: Context | None = None) -> np.ndarray:
+    ctx = ctx or default_context()
+    blocks = np.ascontiguousarray(blocks.ravel())
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    assert blocks.dtype == BLOCK_Q8_0 and a.size == blocks.size * 32
+    out = np.zeros(blocks.size, dtype=np.int32)
+    ctx.check(lib().lgh_q8_block_dots(ctx.handle, _np_ptr(blocks), _np_ptr(a), blocks.size, _np_ptr(out)))
+    return out
+
+
+def q4_mfma_block_dots(w: Q4Matrix, qs: np.ndarray, m: int) -> np.ndarray:
+    """Per-(token, row, block) integer dots via the GEMM's MFMA operand path."""
+    qs = np.ascontiguousarray(qs, dtype=np.int8).reshape(m, w.k)
+    out = np.zeros((m, w.n, w.k // 32), dtype=np.int32)
+    w.ctx.check(lib().lgh_q4_mfma_block_dots(w.ctx.handle, w.handle, _np_ptr(qs), m, _np_ptr(out)))
+    return out

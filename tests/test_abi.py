@@ -1,0 +1,60 @@
+"""The C-ABI library loads without a GPU and exports every declared symbol.
+
+No compute is called here (this runs on machines without a GPU); the only
+calls are ones that never touch a device.
+"""
+
+import ctypes as C
+import re
+
+import pytest
+
+from llmhost_amd import _ffi
+
+
+def _declared_functions():
+    text = open(_ffi.HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lgh_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for must in ("lgh_init", "lgh_q4_upload", "lgh_q4_gemv", "lgh_q4_gemv_pair", "lgh_q4_gemm",
+                 "lgh_q8_gemv", "lgh_act_quant", "lgh_q4_block_dots"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(_ffi.LIB_PATH)
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_ctypes_signatures_cover_the_header():
+    assert set(_declared_functions()) == set(_ffi.SIGNATURES)
+
+
+def test_version_and_null_handling_without_device():
+    lib = _ffi.lib()
+    assert b"gfx950" in lib.lgh_version()
+    # Calls on a null context fail cleanly instead of crashing.
+    assert lib.lgh_sync(None) == _ffi.LGH_ERR_INVALID_ARG
+    assert lib.lgh_set_act_quant(None, 0) == _ffi.LGH_ERR_INVALID_ARG
+    assert lib.lgh_q4_gemv(None, None, None, None, 0) == _ffi.LGH_ERR_INVALID_ARG
+    assert lib.lgh_q4_rows(None) == 0
+    lib.lgh_q4_free(None)
+    lib.lgh_destroy(None)
+
+
+def test_init_reports_missing_device_or_wrong_arch():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; covered by the gpu tests")
+    lib = _ffi.lib()
+    h = C.c_void_p()
+    code = lib.lgh_init(0, C.byref(h))
+    assert code in (_ffi.LGH_ERR_NO_DEVICE, _ffi.LGH_ERR_HIP, _ffi.LGH_ERR_ARCH)
+    assert not h.value
+    assert lib.lgh_last_error(None)

@@ -1,0 +1,314 @@
+"""GPU parity: libllm_gpu_hip.so (through the C ABI) against the CPU oracle.
+
+Bar: bit-exact for integer work (activation codes / scales / sums, per-block
+dots, weight repack and quantize), |gpu - cpu| <= 1e-4 + 1e-5 |cpu| for fp32
+outputs, against the oracle's scalar kernel (the reference operation order)
+and its VNNI kernel (the production CPU path) on identical seeded inputs.
+"""
+
+import numpy as np
+import pytest
+
+from llmhost_amd import q4, synth
+from llmhost_amd.formats import BLOCK_Q4
+
+from .conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- bit-exact integer work ---------------------------------------------------------
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("m,k", [(1, 32), (1, 1536), (3, 8192), (17, 2048), (2, 10752)])
+def test_act_quant_bit_exact(gpu_ctx, oracle, per_row, m, k):
+    x = synth.activations(1000 + k + m, m, k) * np.float32(2.5)
+    x[0, :32] = 0.0                     # zero block
+    if k >= 64:
+        x[-1, 32:36] = [127.0, 2.5, -2.5, 0.5]  # exact ties after scaling by 1/1
+    x = _f32(x)
+    act = (q4.ActQ8.quantize_row if per_row else q4.ActQ8.quantize)(x, gpu_ctx)
+    qs, sc, su = oracle.act_quantize(x, per_row)
+    assert np.array_equal(act.scales.view(np.uint32), sc.view(np.uint32))
+    assert np.array_equal(act.qs, qs)
+    assert np.array_equal(act.sums, su)
+
+
+def test_act_quant_ties(gpu_ctx, oracle):
+    x = np.zeros((1, 64), dtype=np.float32)
+    x[0, :8] = [127.0, 2.5, -2.5, 0.5, -0.5, 126.5, -1.5, 3.5]
+    act = q4.ActQ8.quantize(x, gpu_ctx)
+    assert list(act.qs[0, :8]) == [127, 3, -3, 1, -1, 127, -2, 4]
+    assert act.scales[0, 0] == 1.0 and act.scales[0, 1] == 0.0
+
+
+def _pattern_block(seed):
+    i = np.arange(32)
+    w = (((i * 17 + seed) % 21) - 10).astype(np.float32) * np.float32(0.25)
+    a = (((i * 9 + seed) % 25) - 12).astype(np.int8)
+    return w, a
+
+
+def test_q4_block_dots_bit_exact(gpu_ctx, oracle):
+    # the reference's pattern_block seeds 0..15 (gemv_q4.rs:1080-1102) ...
+    blocks, acts = [], []
+    for seed in range(16):
+        w, a = _pattern_block(seed)
+        blocks.append(oracle.quantize_q4(w)[0])
+        acts.append(a)
+    # ... plus random blocks, extremes and every nibble value
+    rng = np.random.default_rng(1)
+    rb = synth.q4_blocks(77, 256, 32)
+    rb["qs"][0] = 0x88
+    rb["qs"][1] = 0x77
+    blocks.extend(rb)
+    for b in range(256):
+        a = rng.integers(-127, 128, 32, dtype=np.int8)
+        if b in (0, 1):
+            a[:] = -127
+        acts.append(a)
+    blocks = np.array(blocks, dtype=BLOCK_Q4)
+    acts = np.stack(acts)
+    got = q4.q4_block_dots(blocks, acts, gpu_ctx)
+    ref = np.array([oracle.dot_q4_q8(blocks[i], acts[i]) for i in range(len(blocks))])
+    assert np.array_equal(got, ref)
+
+
+def test_q8_block_dots_bit_exact(gpu_ctx, oracle):
+    blocks = synth.q8_blocks(5, 200, 32)
+    blocks["qs"][0] = -127
+    rng = np.random.default_rng(2)
+    acts = rng.integers(-127, 128, (200, 32), dtype=np.int8)
+    acts[0] = -127
+    got = q4.q8_block_dots(blocks, acts, gpu_ctx)
+    ref = np.array([oracle.dot_q8_q8(blocks[i], acts[i]) for i in range(200)])
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("n,k,m", [(48, 64, 40), (17, 96, 5), (70, 256, 33)])
+def test_mfma_block_dots_bit_exact(gpu_ctx, oracle, n, k, m):
+    blocks = synth.q4_blocks(300 + n, n, k)
+    qs = np.random.default_rng(n).integers(-127, 128, (m, k), dtype=np.int8)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = q4.q4_mfma_block_dots(w, qs, m)
+    bpr = k // 32
+    ref = np.zeros((m, n, bpr), dtype=np.int32)
+    for t in range(m):
+        for r in range(n):
+            for b in range(bpr):
+                ref[t, r, b] = oracle.dot_q4_q8(blocks[r * bpr + b], qs[t, b * 32:(b + 1) * 32])
+    assert np.array_equal(got, ref)
+
+
+def test_upload_download_roundtrip(gpu_ctx):
+    blocks = synth.q4_blocks(9, 33, 160)
+    w = q4.Q4Matrix.from_blocks(33, 160, blocks, gpu_ctx)
+    assert w.blocks().tobytes() == blocks.tobytes()
+    b8 = synth.q8_blocks(10, 21, 96)
+    w8 = q4.Q8Matrix.from_blocks(21, 96, b8, gpu_ctx)
+    assert w8.blocks().tobytes() == b8.tobytes()
+
+
+def test_device_quantizers_bit_exact(gpu_ctx, oracle):
+    n, k = 45, 224
+    wf = synth.activations(12, n, k) * np.float32(0.7)
+    wf[0, :32] = 0.0
+    wf[1, :8] = [8.0, -8.0, 2.5, -2.5, 0.5, -0.5, 1.5, -7.5]
+    wf = _f32(wf)
+    assert q4.Q4Matrix.from_f32(wf, n, k, gpu_ctx).blocks().tobytes() == oracle.quantize_q4(wf).tobytes()
+    assert q4.Q8Matrix.from_f32(wf, n, k, gpu_ctx).blocks().tobytes() == oracle.quantize_q8_0(wf).tobytes()
+
+
+# ---- GEMV -----------------------------------------------------------------------------
+GEMV_SHAPES = [(17, 64), (128, 64), (1536, 1536), (8192, 1536), (1536, 8192), (2048, 1536),
+               (1000, 96), (64, 10752), (5, 32), (3, 2080), (4, 65536)]
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+def test_gemv_matches_oracle(gpu_ctx, oracle, n, k):
+    blocks = synth.q4_blocks(10 * n + k, n, k)
+    x = synth.normal_f32(20 * n + k, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = np.zeros(n, dtype=np.float32)
+    q4.gemv_q4(w, x, got)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    assert_close(got, oracle.gemv_q4(mat, x, kernel=oracle.KERNEL_SCALAR, threads=8), what="vs scalar")
+    assert_close(got, oracle.gemv_q4(mat, x, kernel=oracle.KERNEL_VNNI, threads=8), what="vs vnni")
+
+
+def test_gemv_reference_formula_inputs(gpu_ctx, oracle):
+    """gemv_kernels_agree / packed_gemv_matches_block_dots inputs (gemv_q4.rs:1104-1249)."""
+    for n, k, (wm, wmod, wo, ws), (xm, xmod, xo, xs) in [
+            (17, 64, (13, 19, 9, 0.15), (7, 15, 7, 0.2)), (128, 64, (3, 17, 8, 0.1), (5, 11, 5, 0.2))]:
+        w = ((((np.arange(n * k) * wm) % wmod) - wo).astype(np.float32) * np.float32(ws)).astype(np.float32)
+        x = ((((np.arange(k) * xm) % xmod) - xo).astype(np.float32) * np.float32(xs)).astype(np.float32)
+        mat = oracle.Q4Matrix.from_f32(w, n, k)
+        gw = q4.Q4Matrix.from_f32(w, n, k, gpu_ctx)
+        got = np.zeros(n, dtype=np.float32)
+        q4.gemv_q4(gw, x, got)
+        assert_close(got, oracle.gemv_q4(mat, x, kernel=oracle.KERNEL_SCALAR), what=f"n={n}")
+
+
+def test_gemv_add_f64(gpu_ctx, oracle):
+    n, k = 1536, 8192
+    blocks = synth.q4_blocks(5, n, k)
+    x = synth.normal_f32(6, k)
+    y0 = synth.normal_f32(7, n) * np.float32(100.0)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = y0.copy()
+    q4.gemv_q4_add(w, x, got)
+    ref = oracle.gemv_q4(oracle.Q4Matrix(n, k, blocks), x, out=y0.copy(), add=True, threads=8)
+    assert_close(got, ref, what="add_f64")
+    # the epilogue is exactly f32(f64(dst) + f64(W x)) of this kernel's own W x
+    gx = np.zeros(n, dtype=np.float32)
+    q4.gemv_q4(w, x, gx)
+    assert np.array_equal(got, (y0.astype(np.float64) + gx.astype(np.float64)).astype(np.float32))
+
+
+def test_gemv_per_row(gpu_ctx, oracle):
+    n, k = 2048, 1536
+    blocks = synth.q4_blocks(15, n, k)
+    x = synth.normal_f32(16, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow)
+    try:
+        got = np.zeros(n, dtype=np.float32)
+        q4.gemv_q4(w, x, got)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    assert_close(got, oracle.gemv_q4(oracle.Q4Matrix(n, k, blocks), x, per_row=True, threads=8), what="per row")
+
+
+def test_gemv_pair(gpu_ctx, oracle):
+    n, k = 8192, 1536
+    bg, bu = synth.q4_blocks(41, n, k), synth.q4_blocks(42, n, k)
+    x = synth.normal_f32(43, k)
+    wg, wu = q4.Q4Matrix.from_blocks(n, k, bg, gpu_ctx), q4.Q4Matrix.from_blocks(n, k, bu, gpu_ctx)
+    og, ou = np.zeros(n, dtype=np.float32), np.zeros(n, dtype=np.float32)
+    q4.gemv_q4_pair(wg, wu, x, og, ou)
+    rg, ru = oracle.gemv_q4_pair(oracle.Q4Matrix(n, k, bg), oracle.Q4Matrix(n, k, bu), x, threads=8)
+    assert_close(og, rg, what="gate")
+    assert_close(ou, ru, what="up")
+    # pair == two single GEMVs on the GPU
+    sg = np.zeros(n, dtype=np.float32)
+    q4.gemv_q4(wg, x, sg)
+    assert np.array_equal(og, sg)
+
+
+# ---- GEMM -----------------------------------------------------------------------------
+@pytest.mark.parametrize("m,n,k", [(2, 48, 64), (4, 8192, 2048), (16, 512, 2048), (20, 48, 64),
+                                   (40, 48, 64), (64, 1000, 2048), (100, 257, 320), (512, 256, 2048),
+                                   (130, 2048, 10752)])
+def test_gemm_matches_oracle(gpu_ctx, oracle, m, n, k):
+    blocks = synth.q4_blocks(n + 7 * k, n, k)
+    x = synth.activations(m + 3 * k, m, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = np.zeros((m, n), dtype=np.float32)
+    q4.gemm_q4(w, x, got, m)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    assert_close(got, oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_SCALAR, threads=8), what="vs scalar")
+    assert_close(got, oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_VNNI, threads=8), what="vs vnni")
+
+
+def test_gemm_matches_per_token_gemv_reference_inputs(gpu_ctx, oracle):
+    """gemm_matches_per_token_gemv (gemv_q4.rs:1167-1195) and the AMX test (amx.rs:526-557)."""
+    for n, k, m in [(48, 64, 20), (48, 64, 40)]:
+        w = ((((np.arange(n * k) * 3) % 17) - 8).astype(np.float32) * np.float32(0.1)).astype(np.float32)
+        x = ((((np.arange(m * k) * 5) % 11) - 5).astype(np.float32) * np.float32(0.2)).astype(np.float32)
+        gw = q4.Q4Matrix.from_f32(w, n, k, gpu_ctx)
+        gemm = np.zeros(m * n, dtype=np.float32)
+        q4.gemm_q4(gw, x, gemm, m)
+        gemv = np.zeros(m * n, dtype=np.float32)
+        for t in range(m):
+            out = np.zeros(n, dtype=np.float32)
+            q4.gemv_q4(gw, np.ascontiguousarray(x[t * k:(t + 1) * k]), out)
+            gemv[t * n:(t + 1) * n] = out
+        assert np.all(np.abs(gemm - gemv) <= 1e-5 * (1 + np.abs(gemv)))
+        assert_close(gemm.reshape(m, n), oracle.gemm_q4(oracle.Q4Matrix.from_f32(w, n, k), x, m), what="oracle")
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_gemm_add_and_per_row(gpu_ctx, oracle, per_row):
+    m, n, k = 64, 768, 1024
+    blocks = synth.q4_blocks(51, n, k)
+    x = synth.activations(52, m, k)
+    y0 = synth.activations(53, m, n)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        got = y0.copy()
+        q4.gemm_q4_add(w, x, got, m)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    ref = oracle.gemm_q4(oracle.Q4Matrix(n, k, blocks), x, m, out=y0.copy(), add=True, per_row=per_row,
+                         threads=8)
+    assert_close(got, ref, what="gemm add")
+
+
+# ---- Q8_0 GEMV ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,k,tokens", [(1536, 1536, 1), (77, 256, 3), (4096, 1536, 2)])
+def test_q8_gemv_matches_oracle(gpu_ctx, oracle, n, k, tokens):
+    blocks = synth.q8_blocks(n + k, n, k)
+    x = synth.activations(tokens + k, tokens, k)
+    w = q4.Q8Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = np.zeros((tokens, n) if tokens > 1 else n, dtype=np.float32)
+    q4.q8_apply(w, x, tokens, got)
+    assert_close(got, oracle.q8_apply(blocks, n, k, x, tokens, threads=8), what="q8")
+
+
+# ---- error behaviour --------------------------------------------------------------------------
+def test_shape_errors(gpu_ctx):
+    with pytest.raises(q4.LghShapeError):
+        q4.Q4Matrix.from_blocks(4, 48, np.zeros(6, dtype=BLOCK_Q4), gpu_ctx)
+    w = q4.Q4Matrix.from_blocks(8, 64, synth.q4_blocks(1, 8, 64), gpu_ctx)
+    with pytest.raises(q4.LghShapeError):
+        q4.gemv_q4(w, np.zeros(32, dtype=np.float32), np.zeros(8, dtype=np.float32))
+    with pytest.raises(q4.LghShapeError):
+        q4.gemm_q4(w, np.zeros(64 * 3, dtype=np.float32), np.zeros(8 * 2, dtype=np.float32), 3)
+    w2 = q4.Q4Matrix.from_blocks(16, 64, synth.q4_blocks(2, 16, 64), gpu_ctx)
+    with pytest.raises(q4.LghShapeError):
+        q4.gemv_q4_pair(w, w2, np.zeros(64, dtype=np.float32), np.zeros(8, dtype=np.float32),
+                        np.zeros(16, dtype=np.float32))
+
+
+def test_empty_is_noop(gpu_ctx):
+    w = q4.Q4Matrix.from_blocks(0, 64, np.zeros(0, dtype=BLOCK_Q4), gpu_ctx)
+    q4.gemv_q4(w, np.zeros(64, dtype=np.float32), np.zeros(0, dtype=np.float32))
+    w2 = q4.Q4Matrix.from_blocks(8, 64, synth.q4_blocks(1, 8, 64), gpu_ctx)
+    out = np.full((0, 8), 3.0, dtype=np.float32)
+    q4.gemm_q4(w2, np.zeros((0, 64), dtype=np.float32), out, 0)
+
+
+# ---- device pointers (torch tensors) ------------------------------------------------------------
+def test_device_pointer_path_matches_host_path(gpu_ctx):
+    import torch
+
+    n, k, m = 4096, 2048, 24
+    blocks = synth.q4_blocks(61, n, k)
+    x = synth.activations(62, m, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    host1 = np.zeros(n, dtype=np.float32)
+    q4.gemv_q4(w, np.ascontiguousarray(x[0]), host1)
+    hostm = np.zeros((m, n), dtype=np.float32)
+    q4.gemm_q4(w, x, hostm, m)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        xd = torch.from_numpy(x).cuda()
+        y1 = torch.zeros(n, device="cuda")
+        ym = torch.zeros(m, n, device="cuda")
+        gpu_ctx.set_stream(stream.cuda_stream)
+        try:
+            q4.gemv_q4(w, xd[0], y1)
+            q4.gemm_q4(w, xd, ym, m)
+            stream.synchronize()
+        finally:
+            gpu_ctx.set_stream(None)
+    assert np.array_equal(y1.cpu().numpy(), host1)
+    assert np.array_equal(ym.cpu().numpy(), hostm)
+    # device-resident raw blocks upload
+    bd = torch.from_numpy(blocks.view(np.uint8).copy()).cuda()
+    wd = q4.Q4Matrix.from_blocks(n, k, bd, gpu_ctx)
+    assert wd.blocks().tobytes() == blocks.tobytes()
