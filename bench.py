@@ -77,17 +77,32 @@ class GpuBench:
         return blocks, mats
 
     def timed(self, fn, iters, warmup):
+        """ms per iteration of fn(i), i = 0..iters-1, replayed from a HIP graph.
+
+        The warm-up runs eagerly (it also sizes every workspace, so nothing is
+        allocated under capture); the timed region is one replay of a graph
+        holding all `iters` iterations, bracketed by device synchronisation
+        and HIP events on the stream the library launches on.
+        """
         torch = self.torch
         with torch.cuda.stream(self.stream):
             for i in range(warmup):
                 fn(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=self.stream):
+            for i in range(iters):
+                fn(i)
+        # replay() launches on torch's current stream: make it the library's.
+        with torch.cuda.stream(self.stream):
+            graph.replay()  # first replay uploads the graph
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(self.stream)
-            for i in range(iters):
-                fn(i)
+            graph.replay()
             e1.record(self.stream)
-            torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        del graph
         return e0.elapsed_time(e1) / iters  # ms per iteration
 
 

@@ -80,10 +80,6 @@ struct Carve {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Largest K the fused GEMV keeps in LDS (32 B + 4 B per block, 64 KiB);
-// longer rows run through the batched act-quant + GEMM path with m = 1.
-constexpr size_t kGemvMaxBpr = (65536 - 64) / 36;
-
 template <class M>
 int alloc_matrix(lgh_ctx *ctx, size_t n, size_t k, size_t qs_bytes_per_block, M **out) {
   auto *w = new (std::nothrow) M();
@@ -333,6 +329,18 @@ static int check_mode(lgh_ctx *ctx, int mode) {
 
 int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode);
 
+static int launch_gemv(lgh_ctx *ctx, const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
+                       int mode) {
+  if (!lgh::plan_q4_gemv(w0->n, w0->bpr, w1 ? 2 : 1).ok) {
+    // K longer than the GEMV covers: batched act-quant + GEMM with m = 1.
+    if (int r = lgh_q4_gemm_dev(ctx, w0, x, y0, 1, mode)) return r;
+    return w1 ? lgh_q4_gemm_dev(ctx, w1, x, y1, 1, mode) : LGH_OK;
+  }
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_q4_gemv(w0, y0, w1, y1, x, mode, ctx->act_mode, ctx->stream));
+  return LGH_OK;
+}
+
 int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
@@ -340,10 +348,7 @@ int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  if (w->bpr > kGemvMaxBpr) return lgh_q4_gemm_dev(ctx, w, x_dev, y_dev, 1, mode);
-  if (int r = set_device(ctx)) return r;
-  LGH_HIP(ctx, lgh::launch_q4_gemv(w, y_dev, nullptr, nullptr, x_dev, mode, ctx->act_mode, ctx->stream));
-  return LGH_OK;
+  return launch_gemv(ctx, w, y_dev, nullptr, nullptr, x_dev, mode);
 }
 
 int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const float *x_dev, float *yg_dev,
@@ -356,13 +361,7 @@ int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const
   if (wg->n == 0) return LGH_OK;
   if (!yg_dev || !yu_dev || (wg->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  if (wg->bpr > kGemvMaxBpr) {
-    if (int r = lgh_q4_gemm_dev(ctx, wg, x_dev, yg_dev, 1, LGH_ASSIGN)) return r;
-    return lgh_q4_gemm_dev(ctx, wu, x_dev, yu_dev, 1, LGH_ASSIGN);
-  }
-  if (int r = set_device(ctx)) return r;
-  LGH_HIP(ctx, lgh::launch_q4_gemv(wg, yg_dev, wu, yu_dev, x_dev, LGH_ASSIGN, ctx->act_mode, ctx->stream));
-  return LGH_OK;
+  return launch_gemv(ctx, wg, yg_dev, wu, yu_dev, x_dev, LGH_ASSIGN);
 }
 
 int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
@@ -372,7 +371,7 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  if (m == 1 && w->bpr <= kGemvMaxBpr) return lgh_q4_gemv_dev(ctx, w, x_dev, y_dev, mode);
+  if (m == 1 && lgh::plan_q4_gemv(w->n, w->bpr, 1).ok) return lgh_q4_gemv_dev(ctx, w, x_dev, y_dev, mode);
   if (int r = set_device(ctx)) return r;
   Carve cv;
   const size_t o_qs = cv.take(m * w->k);
@@ -394,7 +393,7 @@ int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_
   if (tokens == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  if (w->bpr > kGemvMaxBpr) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", kGemvMaxBpr * 32);
+  if (w->k > lgh::kQ8GemvMaxK) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", lgh::kQ8GemvMaxK);
   if (tokens > 65535) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports at most 65535 tokens per call");
   if (int r = set_device(ctx)) return r;
   LGH_HIP(ctx, lgh::launch_q8_gemv(w, x_dev, y_dev, tokens, ctx->stream));

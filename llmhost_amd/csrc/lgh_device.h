@@ -19,6 +19,75 @@ __device__ __forceinline__ uint4 load_nt16(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---- raw buffer loads ------------------------------------------------------
+// A buffer resource covers [base, base + bytes); a load whose byte offset is
+// out of that range returns 0 (hardware range check), so tails and padding
+// need no branches and every load of a lane can be issued back to back.
+// kOOB is an offset that is always out of range.  `base` must be uniform
+// across the wave (it lives in scalar registers).
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kBufDword3 = 0x00020000;  // gfx9-family raw buffer: 32-bit data, no swizzle
+constexpr int kAuxNT = 2;               // nontemporal (streaming) hint
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), kBufDword3);
+}
+
+template <int Aux = 0>
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, Aux);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0);
+  return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ float4 buf_load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  // Bit-cast the whole vector: this clang reads element 0 for every
+  // __builtin_bit_cast(float, v.y)-style cast of a single vector element.
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
+}
+
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0));
+}
+
+// Wave-uniform value as a scalar (the compiler cannot prove threadIdx.x / 64
+// uniform by itself).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---- DPP wave64 sum --------------------------------------------------------
+template <int Ctrl, int RowMask = 0xf>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, RowMask,
+                                                               0xf, false));
+}
+
+// Sum over the 64 lanes, result valid in every lane: DPP within rows of 16
+// (quad_perm 1032, quad_perm 2301, row_half_mirror, row_mirror), then the 4
+// row partials are read as scalars and added.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror: lane i <-> 7-i within 8
+  v += dpp<0x140>(v);  // row_mirror: lane i <-> 15-i within 16
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // f16 bits -> f32, exact (v_cvt_f32_f16; every binary16 value is a binary32
 // value), matching half::f16::to_f32.
 __device__ __forceinline__ float h2f(uint16_t h) {
@@ -92,30 +161,65 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---- exact fast divisions for ActQ8 -----------------------------------------
+// RN(a / 127) for every finite a >= 0: q0 = a*y with y = RN(1/127), then one
+// Markstein correction q = fma(fma(-q0, 127, a), y, q0).  Proven exhaustively
+// over all 2^31 non-negative floats (denormals included) by
+// tests/fastquant_check.c.
+__device__ __forceinline__ float div127_rn(float a) {
+  const float y = 0x1.020408p-7f;  // RN(1/127)
+  const float q0 = a * y;
+  return fmaf(fmaf(-q0, 127.0f, a), y, q0);
+}
+
+// RN(1 / s) for s > 0: v_rcp_f32 (faithful, 1 ulp) refined by one FMA Newton
+// step, which tests/fastquant_check.c proves correctly rounded for either
+// faithful starting value for every s in [2^-126, 2^126) except the
+// all-ones significand; those and out-of-range s use the IEEE division.
+__device__ __forceinline__ float recip_rn(float s) {
+  const float y0 = __builtin_amdgcn_rcpf(s);
+  float q = fmaf(fmaf(-s, y0, 1.0f), y0, y0);
+  const uint32_t b = __builtin_bit_cast(uint32_t, s);
+  if (b < 0x00800000u || b >= 0x7E800000u || (b & 0x7FFFFFu) == 0x7FFFFFu) q = __fdiv_rn(1.0f, s);
+  return q;
+}
+
+// clamp(round_half_away_from_zero(v * inv), -127, 127) from inv2 = 2 * inv:
+// i = trunc(2y) exactly (RN(v * 2inv) = 2 RN(v * inv)), and for an integer
+// i = trunc(2y), round_half_away(y) = (i + (i < 0 ? -1 : 0) + 1) >> 1 with an
+// arithmetic shift (y >= 0: floor((floor(2y) + 1) / 2); y < 0: floor(i / 2)).
+// NaN converts to 0, like Rust's `NaN as i8`.
+__device__ __forceinline__ int quant_code(float v, float inv2) {
+  const int i = static_cast<int>(v * inv2);  // v_cvt_i32_f32 truncates
+  const int q = (i + (i >> 31) + 1) >> 1;
+  return min(max(q, -127), 127);
+}
+
 // ActQ8 quantization of one 32-element block by a group of 8 lanes
 // (crates/llm-cpu/src/gemv_q4.rs:77-94).  Lane j of the group holds elements
 // 4j..4j+3 in v.  Returns the packed int8 codes for those 4 elements; writes
 // the block scale and the block sum of codes (valid in every group lane).
-//   scale = amax / 127            (f32, correctly rounded)
-//   inv   = scale == 0 ? 0 : 1/scale  (f32, correctly rounded)
+//   scale = amax / 127               (f32, correctly rounded)
+//   inv   = scale == 0 ? 0 : 1/scale (f32, correctly rounded)
 //   q     = clamp(round_half_away_from_zero(v * inv), -127, 127)
 // With per_row, `row_scale` (= row amax / 127) replaces the block scale.
 __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float row_scale, float &scale,
                                                 int &sum) {
+  // 8-lane max/sum by DPP: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror.
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-  scale = per_row ? row_scale : __fdiv_rn(amax, 127.0f);
-  const float inv = scale == 0.0f ? 0.0f : __fdiv_rn(1.0f, scale);
-  const int q0 = static_cast<int>(fminf(fmaxf(roundf(v.x * inv), -127.0f), 127.0f));
-  const int q1 = static_cast<int>(fminf(fmaxf(roundf(v.y * inv), -127.0f), 127.0f));
-  const int q2 = static_cast<int>(fminf(fmaxf(roundf(v.z * inv), -127.0f), 127.0f));
-  const int q3 = static_cast<int>(fminf(fmaxf(roundf(v.w * inv), -127.0f), 127.0f));
+  amax = fmaxf(amax, dpp<0xB1>(amax));
+  amax = fmaxf(amax, dpp<0x4E>(amax));
+  amax = fmaxf(amax, dpp<0x141>(amax));
+  scale = per_row ? row_scale : div127_rn(amax);
+  const float inv2 = scale == 0.0f ? 0.0f : 2.0f * recip_rn(scale);
+  const int q0 = quant_code(v.x, inv2);
+  const int q1 = quant_code(v.y, inv2);
+  const int q2 = quant_code(v.z, inv2);
+  const int q3 = quant_code(v.w, inv2);
   int s = q0 + q1 + q2 + q3;
-  s += __shfl_xor(s, 1, 8);
-  s += __shfl_xor(s, 2, 8);
-  s += __shfl_xor(s, 4, 8);
+  s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xf, 0xf, false);
+  s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xf, 0xf, false);
+  s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xf, 0xf, false);
   sum = s;
   return (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (static_cast<int>(static_cast<uint32_t>(q3) << 24));
 }

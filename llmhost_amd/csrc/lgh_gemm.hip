@@ -58,46 +58,54 @@ template <class C>
 struct Stage {
   uint4 w[C::W_LD];
   uint4 a[C::A_LD];
-  float sw[C::SW_LD];
+  uint16_t sw[C::SW_LD];  // f16 bits; converted when written to LDS
   float sa[C::SA_LD];
 };
 
+// Issue every global load of one K chunk, all branch-free raw buffer loads.
+// The resources cover this workgroup's operand panels: rows beyond n / m fall
+// outside them and load as 0; blocks beyond bpr get kOOB offsets.  They are
+// rebuilt from scalars here (kernel arguments and blockIdx) so the compiler
+// keeps them in SGPRs.
 template <class C>
 __device__ __forceinline__ void load_chunk(const GemmArgs &g, int n0, int m0, int kb0, Stage<C> &s) {
   const int tid = threadIdx.x;
+  // readfirstlane: the clamps select to VALU med3, which would otherwise put
+  // the resource sizes in VGPRs (and every load in a waterfall loop).
+  const uint32_t rn = static_cast<uint32_t>(uniform(max(0, min(C::BN, g.n - n0))));
+  const uint32_t rm = static_cast<uint32_t>(uniform(max(0, min(C::BM, g.m - m0))));
+  const size_t wb = static_cast<size_t>(n0) * g.bpr, ab = static_cast<size_t>(m0);
+  const auto pw = make_rsrc(g.qs + wb * 16, rn * g.bpr * 16u);
+  const auto psw = make_rsrc(g.sc + wb, rn * g.bpr * 2u);
+  const auto pa = make_rsrc(g.aq + ab * g.k, rm * static_cast<uint32_t>(g.k));
+  const auto psa = make_rsrc(g.sa + ab * g.bpr, rm * g.bpr * 4u);
 #pragma unroll
   for (int i = 0; i < C::W_LD; i++) {
     const int c = tid + i * kThreads;  // c -> (row, q): 4 threads cover a row's 64 B
-    const int row = c / KC, q = c % KC;
-    const int n = n0 + row, kb = kb0 + q;
-    s.w[i] = (c < C::BN * KC && n < g.n && kb < g.bpr)
-                 ? load_nt16(reinterpret_cast<const uint4 *>(g.qs) + (static_cast<size_t>(n) * g.bpr + kb))
-                 : make_uint4(0, 0, 0, 0);
+    const int row = c / KC, kb = kb0 + c % KC;
+    const bool ok = c < C::BN * KC && kb < g.bpr;
+    s.w[i] = buf_load16<kAuxNT>(pw, ok ? static_cast<uint32_t>(row * g.bpr + kb) * 16u : kOOB);
   }
 #pragma unroll
   for (int i = 0; i < C::SW_LD; i++) {
     const int c = tid + i * kThreads;
-    const int row = c / KC, q = c % KC;
-    const int n = n0 + row, kb = kb0 + q;
-    s.sw[i] = (c < C::BN * KC && n < g.n && kb < g.bpr) ? h2f(g.sc[static_cast<size_t>(n) * g.bpr + kb])
-                                                        : 0.0f;
+    const int row = c / KC, kb = kb0 + c % KC;
+    const bool ok = c < C::BN * KC && kb < g.bpr;
+    s.sw[i] = buf_load_u16(psw, ok ? static_cast<uint32_t>(row * g.bpr + kb) * 2u : kOOB);
   }
 #pragma unroll
   for (int i = 0; i < C::A_LD; i++) {
     const int c = tid + i * kThreads;  // c -> (row, q, h): 8 threads cover a row's 128 B
     const int row = c / (KC * 2), qh = c % (KC * 2);
-    const int m = m0 + row, kb = kb0 + qh / 2;
-    s.a[i] = (c < C::BM * KC * 2 && m < g.m && kb < g.bpr)
-                 ? *reinterpret_cast<const uint4 *>(g.aq + static_cast<size_t>(m) * g.k +
-                                                    static_cast<size_t>(kb0) * 32 + qh * 16)
-                 : make_uint4(0, 0, 0, 0);
+    const bool ok = c < C::BM * KC * 2 && kb0 + qh / 2 < g.bpr;
+    s.a[i] = buf_load16(pa, ok ? static_cast<uint32_t>(row * g.k + kb0 * 32 + qh * 16) : kOOB);
   }
 #pragma unroll
   for (int i = 0; i < C::SA_LD; i++) {
     const int c = tid + i * kThreads;
-    const int row = c / KC, q = c % KC;
-    const int m = m0 + row, kb = kb0 + q;
-    s.sa[i] = (c < C::BM * KC && m < g.m && kb < g.bpr) ? g.sa[static_cast<size_t>(m) * g.bpr + kb] : 0.0f;
+    const int row = c / KC, kb = kb0 + c % KC;
+    const bool ok = c < C::BM * KC && kb < g.bpr;
+    s.sa[i] = buf_load_f32(psa, ok ? static_cast<uint32_t>(row * g.bpr + kb) * 4u : kOOB);
   }
 }
 
@@ -120,7 +128,7 @@ __device__ __forceinline__ void store_chunk(char *lds, const Stage<C> &s) {
 #pragma unroll
   for (int i = 0; i < C::SW_LD; i++) {
     const int c = tid + i * kThreads;
-    if (c < C::BN * KC) s_sw[(c % KC) * C::BN + c / KC] = s.sw[i];
+    if (c < C::BN * KC) s_sw[(c % KC) * C::BN + c / KC] = h2f(s.sw[i]);
   }
 #pragma unroll
   for (int i = 0; i < C::A_LD; i++) {
@@ -169,7 +177,9 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mfma_kernel(GemmArgs g) {
 
   for (int ch = 0; ch < nchunks; ch++) {
     if (ch + 1 < nchunks) load_chunk<C>(g, n0, m0, (ch + 1) * KC, st);
-#pragma unroll
+    // Not unrolled: unrolling lets the scheduler hoist all KC*TN*TM MFMAs and
+    // keep their 16-register results live at once (register spills).
+#pragma unroll 1
     for (int q = 0; q < KC; q++) {
       v4i A[TN], B[TM];
 #pragma unroll

@@ -71,8 +71,17 @@ hipError_t launch_q8_quantize(const float *w, size_t nblocks, int8_t *qs, uint16
                               hipStream_t stream);
 
 // GEMV: y = W x for one or two matrices sharing x (pair).  w1 may be null.
+// plan.ok is false when K is longer than one workgroup covers (K > 32768):
+// the API then runs the batched act-quant + GEMM path with m = 1.
+struct Q4GemvPlan {
+  int R, S, KW, wgs_per_mat;
+  bool ok;
+};
+Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);
+// Q8_0 GEMV for k <= kQ8GemvMaxK.
+constexpr size_t kQ8GemvMaxK = 12288;
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens,
                           hipStream_t stream);
 

@@ -312,3 +312,67 @@ def test_device_pointer_path_matches_host_path(gpu_ctx):
     bd = torch.from_numpy(blocks.view(np.uint8).copy()).cuda()
     wd = q4.Q4Matrix.from_blocks(n, k, bd, gpu_ctx)
     assert wd.blocks().tobytes() == blocks.tobytes()
+
+
+# ---- HIP graph replay and split-K determinism -------------------------------------------------
+def test_split_k_gemv_is_deterministic(gpu_ctx, oracle):
+    n, k = 1536, 10752  # several K slices
+    blocks = synth.q4_blocks(81, n, k)
+    x = synth.normal_f32(82, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    outs = []
+    for _ in range(3):
+        y = np.zeros(n, dtype=np.float32)
+        q4.gemv_q4(w, x, y)
+        outs.append(y)
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert_close(outs[0], oracle.gemv_q4(oracle.Q4Matrix(n, k, blocks), x, threads=8), what="split-K")
+
+
+def test_graph_replay_matches_eager(gpu_ctx):
+    """Capture GEMV (one slice and split-K), pair, AddF64 and GEMM into one
+    graph; replay it several times with eager work in between and check every
+    replay bit-exactly against the eager results."""
+    import torch
+
+    shapes = {"up": (8192, 1536), "down": (1536, 8192)}
+    mats = {k: q4.Q4Matrix.from_blocks(n, kk, synth.q4_blocks(90 + i, n, kk), gpu_ctx)
+            for i, (k, (n, kk)) in enumerate(shapes.items())}
+    gate = q4.Q4Matrix.from_blocks(8192, 1536, synth.q4_blocks(95, 8192, 1536), gpu_ctx)
+    stream = torch.cuda.Stream()
+    gpu_ctx.set_stream(stream.cuda_stream)
+    try:
+        with torch.cuda.stream(stream):
+            x1 = torch.from_numpy(synth.normal_f32(96, 1536)).cuda()
+            x2 = torch.from_numpy(synth.normal_f32(97, 8192)).cuda()
+            xm = torch.from_numpy(synth.activations(98, 64, 1536)).cuda()
+            y0 = torch.from_numpy(synth.normal_f32(99, 1536)).cuda()
+            outs = {"up": torch.empty(8192, device="cuda"), "g": torch.empty(8192, device="cuda"),
+                    "u": torch.empty(8192, device="cuda"), "down": torch.empty(1536, device="cuda"),
+                    "gemm": torch.empty(64, 8192, device="cuda")}
+
+            def run():
+                q4.gemv_q4(mats["up"], x1, outs["up"])
+                q4.gemv_q4_pair(gate, mats["up"], x1, outs["g"], outs["u"])
+                outs["down"].copy_(y0)
+                q4.gemv_q4_add(mats["down"], x2, outs["down"])
+                q4.gemm_q4(mats["up"], xm, outs["gemm"], 64)
+
+            run()
+            stream.synchronize()
+            eager = {k: v.clone() for k, v in outs.items()}
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                run()
+            for rep in range(3):
+                for v in outs.values():
+                    v.fill_(float("nan"))
+                scratch = torch.empty(1536, device="cuda")
+                q4.gemv_q4(mats["down"], x2, scratch)  # eager work between replays
+                graph.replay()
+                stream.synchronize()
+                for k, v in outs.items():
+                    assert torch.equal(v, eager[k]), f"replay {rep}: {k} differs"
+            del graph
+    finally:
+        gpu_ctx.set_stream(None)
