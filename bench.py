@@ -244,6 +244,36 @@ def cpu_baseline(target_s: float = 12.0):
             "ms_per_step": el / steps * 1e3}
 
 
+def counters_mode(iters: int = 50) -> None:
+    """Eager launches for hardware-counter runs (rocprofv3 --pmc): `iters`
+    launches of each headline GEMV over rotating copies, then a plain 64 MiB
+    device-to-device copy (torch) of known size to calibrate FETCH_SIZE /
+    WRITE_SIZE against.  Prints the byte counts each kernel should move."""
+    gb = GpuBench()
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    for i, (name, n, k) in enumerate([("up", 8192, 1536), ("down", 1536, 8192)]):
+        _, mats = gb.copies(n, k, 101 + i, 2 * MALL_BYTES + (64 << 20))
+        x = torch.from_numpy(synth.normal_f32(201 + i, k)).cuda()
+        y = torch.zeros(n, device="cuda")
+        with torch.cuda.stream(gb.stream):
+            for it in range(iters):
+                q4.gemv_q4(mats[it % len(mats)], x, y)
+        torch.cuda.synchronize()
+        log(f"[counters] {name}: {iters} launches, algorithmic bytes/launch {q4_bytes(n, k)} "
+            f"(weights {n * (k // 32) * 18})")
+        for w in mats:
+            w.free()
+    src = torch.ones(16 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    with torch.cuda.stream(gb.stream):
+        for _ in range(iters):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[counters] copy: {iters} launches of a 64 MiB read + 64 MiB write")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,10 +281,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only")
+    ap.add_argument("--counters", action="store_true",
+                    help="eager launches for rocprofv3 --pmc runs (no JSON line)")
     args = ap.parse_args()
+    if args.counters:
+        counters_mode()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the hot path is a "
-              "single-GPU kernel; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "single-GPU kernel; a multi-GPU split would shard weight rows by N and is not "
+              "built)", file=sys.stderr)
         sys.exit(2)
 
     gb = GpuBench()
