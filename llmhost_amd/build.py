@@ -19,7 +19,9 @@ SOURCES = ["lgh_api.hip", "lgh_gemv.hip", "lgh_gemm.hip", "lgh_quant.hip"]
 ARCH = "gfx950"
 
 # Packed FP32 VALU ops are disabled on purpose: every kernel here is written
-# against plain fp32 VALU instructions.
+# against plain fp32 VALU instructions.  MFMA results go to arch VGPRs (not
+# AGPRs): the GEMM folds every MFMA result with VALU FMAs, and AGPR results
+# would cost a v_accvgpr_read per element.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -28,6 +30,7 @@ HIP_FLAGS = [
     "-shared",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -7,6 +7,7 @@
 // on lengths, k % 32); here every such case returns LGH_ERR_SHAPE (or
 // LGH_ERR_INVALID_ARG for null/misaligned pointers) before any work is
 // enqueued, and lgh_last_error() names the violated condition.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -106,17 +107,39 @@ int alloc_matrix(lgh_ctx *ctx, size_t n, size_t k, size_t qs_bytes_per_block, M 
   return LGH_OK;
 }
 
+void free_extra(lgh_q8 *) {}
+void free_extra(lgh_q4 *w) {
+  if (w->mx) (void)hipFree(w->mx);
+}
+
 template <class M>
 void free_matrix(M *w) {
   if (!w) return;
-  if (w->qs) {
-    int cur = 0;
-    (void)hipGetDevice(&cur);
-    (void)hipSetDevice(w->device);
-    (void)hipFree(w->qs);
-    (void)hipSetDevice(cur);
-  }
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(w->device);
+  if (w->qs) (void)hipFree(w->qs);
+  free_extra(w);
+  (void)hipSetDevice(cur);
   delete w;
+}
+
+// GEMM operand image of a Q4 matrix, built from its nibble/scale planes.
+// Matrices whose image would not fit 31-bit buffer offsets keep mx = null;
+// the GEMV path serves them and the GEMM entry points report LGH_ERR_SHAPE.
+int build_mx(lgh_ctx *ctx, lgh_q4 *w) {
+  w->nt = (w->n + 31) / 32;
+  w->pp = (w->bpr + 1) / 2;
+  const size_t bytes = w->nt * w->pp * lgh::kMxWRec;
+  if (!bytes || (w->nt + 8) * w->pp * lgh::kMxWRec >= lgh::kMxMaxBytes) return LGH_OK;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess)
+    return fail(ctx, LGH_ERR_OOM, "hipMalloc(%zu bytes) for the GEMM operand image failed: %s", bytes,
+                hipGetErrorString(e));
+  w->mx = static_cast<uint8_t *>(p);
+  LGH_HIP(ctx, lgh::launch_q4_mx_pack(w, ctx->stream));
+  return LGH_OK;
 }
 
 int check_shape(lgh_ctx *ctx, const void *p, size_t n, size_t k, void *out) {
@@ -204,6 +227,23 @@ int lgh_sync(lgh_ctx *ctx) {
 }
 
 // ---- weights -------------------------------------------------------------
+namespace {
+// Build the GEMM image of a freshly repacked matrix and wait for the upload.
+int finish_q4(lgh_ctx *ctx, lgh_q4 *w, lgh_q4 **out) {
+  int r = build_mx(ctx, w);
+  if (r == LGH_OK) {
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) r = hip_fail(ctx, e, "Q4 upload");
+  }
+  if (r != LGH_OK) {
+    free_matrix(w);
+    return r;
+  }
+  *out = w;
+  return LGH_OK;
+}
+}  // namespace
+
 int lgh_q4_upload_dev(lgh_ctx *ctx, const void *blocks_dev, size_t n, size_t k, lgh_q4 **out) {
   if (int r = check_shape(ctx, blocks_dev, n, k, out)) return r;
   if (int r = set_device(ctx)) return r;
@@ -211,13 +251,11 @@ int lgh_q4_upload_dev(lgh_ctx *ctx, const void *blocks_dev, size_t n, size_t k, 
   if (int r = alloc_matrix(ctx, n, k, 16, &w)) return r;
   hipError_t e = lgh::launch_q4_repack(static_cast<const uint8_t *>(blocks_dev), n * w->bpr, w->qs, w->sc,
                                        ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
     free_matrix(w);
     return hip_fail(ctx, e, "Q4 repack");
   }
-  *out = w;
-  return LGH_OK;
+  return finish_q4(ctx, w, out);
 }
 
 int lgh_q4_upload(lgh_ctx *ctx, const void *blocks, size_t n, size_t k, lgh_q4 **out) {
@@ -239,13 +277,11 @@ int lgh_q4_from_f32(lgh_ctx *ctx, const float *wf, size_t n, size_t k, lgh_q4 **
   hipError_t e = bytes ? hipMemcpyAsync(ctx->stage, wf, bytes, hipMemcpyHostToDevice, ctx->stream) : hipSuccess;
   if (e == hipSuccess)
     e = lgh::launch_q4_quantize(static_cast<const float *>(ctx->stage), n * w->bpr, w->qs, w->sc, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
     free_matrix(w);
     return hip_fail(ctx, e, "Q4 quantize");
   }
-  *out = w;
-  return LGH_OK;
+  return finish_q4(ctx, w, out);
 }
 
 int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks) {
@@ -372,18 +408,29 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
   if (m == 1 && lgh::plan_q4_gemv(w->n, w->bpr, 1).ok) return lgh_q4_gemv_dev(ctx, w, x_dev, y_dev, mode);
+  if (!w->mx) return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w->n, w->k);
   if (int r = set_device(ctx)) return r;
+  // Tokens per launch: the activation image must fit 31-bit buffer offsets.
+  const size_t rec_per_tile = w->pp * lgh::kMxARec;
+  const size_t cap_tiles = lgh::kMxMaxBytes / rec_per_tile;
+  if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", w->k);
+  const size_t chunk = std::min(m, (cap_tiles - 8) * 32);
+  const int splits = lgh::plan_q4_gemm_splits(w, chunk);
   Carve cv;
-  const size_t o_qs = cv.take(m * w->k);
-  const size_t o_sa = cv.take(m * w->bpr * sizeof(float));
-  const size_t o_rs = cv.take(m * sizeof(float));
+  const size_t o_mx = cv.take((chunk + 31) / 32 * rec_per_tile);
+  const size_t o_rs = cv.take(chunk * sizeof(float));
+  const size_t part_floats = splits > 1 ? splits * chunk * w->n : 0;
+  const size_t o_part = cv.take(part_floats * sizeof(float));
   if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
   char *ws = static_cast<char *>(ctx->ws);
-  auto *qs = reinterpret_cast<int8_t *>(ws + o_qs);
-  auto *sa = reinterpret_cast<float *>(ws + o_sa);
+  auto *mxa = reinterpret_cast<uint8_t *>(ws + o_mx);
   auto *rs = reinterpret_cast<float *>(ws + o_rs);
-  LGH_HIP(ctx, lgh::launch_act_quant(x_dev, m, w->k, ctx->act_mode, qs, sa, nullptr, rs, ctx->stream));
-  LGH_HIP(ctx, lgh::launch_q4_gemm(w, qs, sa, y_dev, m, mode, ctx->stream));
+  auto *part = reinterpret_cast<float *>(ws + o_part);
+  for (size_t m0 = 0; m0 < m; m0 += chunk) {
+    const size_t mc = std::min(chunk, m - m0);
+    LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * w->k, mc, w->k, ctx->act_mode, mxa, rs, ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemm(w, mxa, y_dev + m0 * w->n, mc, mode, part, part_floats, ctx->stream));
+  }
   return LGH_OK;
 }
 
@@ -545,14 +592,18 @@ int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size
   if (m == 0 || w->n == 0 || w->bpr == 0) return LGH_OK;
   if (!qs || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
   if (int r = set_device(ctx)) return r;
+  if (!w->mx) return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w->n, w->k);
   const size_t ob_bytes = m * w->n * w->bpr * 4;
+  const size_t mx_bytes = (m + 31) / 32 * w->pp * lgh::kMxARec;
+  if (mx_bytes >= lgh::kMxMaxBytes) return fail(ctx, LGH_ERR_SHAPE, "too many tokens for one hook call");
   Carve cv;
-  const size_t oq = cv.take(m * w->k), oo = cv.take(ob_bytes);
+  const size_t oq = cv.take(m * w->k), omx = cv.take(mx_bytes), oo = cv.take(ob_bytes);
   if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
   char *st = static_cast<char *>(ctx->stage);
+  auto *mxa = reinterpret_cast<uint8_t *>(st + omx);
   LGH_HIP(ctx, hipMemcpyAsync(st + oq, qs, m * w->k, hipMemcpyHostToDevice, ctx->stream));
-  LGH_HIP(ctx, lgh::launch_q4_mfma_block_dots(w, reinterpret_cast<int8_t *>(st + oq), m,
-                                              reinterpret_cast<int32_t *>(st + oo), ctx->stream));
+  LGH_HIP(ctx, lgh::launch_act_split_mx(reinterpret_cast<int8_t *>(st + oq), m, w->k, mxa, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q4_mfma_block_dots(w, mxa, m, reinterpret_cast<int32_t *>(st + oo), ctx->stream));
   LGH_HIP(ctx, hipMemcpyAsync(out, st + oo, ob_bytes, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return LGH_OK;

@@ -224,4 +224,89 @@ __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float ro
   return (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (static_cast<int>(static_cast<uint32_t>(q3) << 24));
 }
 
+// ---- MX-fp6 operand codes ----------------------------------------------------
+// The GEMM feeds integer operands to the fp6 matrix cores as OCP MX FP6 E3M2
+// codes (1 sign, 3 exponent bits with bias 3, 2 mantissa bits).  Every
+// integer in [-8, 8] is exact in E3M2, so a Q4 weight (-8..7) is one code and
+// an int8 activation q (-127..127) is two: q = 16 h + l with
+// h = (q + 8) >> 4 in [-8, 8] and l = q - 16 h in [-8, 7].
+// An MFMA operand row holds 32 codes packed densely, code t in bits
+// [6t, 6t + 6) of six dwords.  Stored as two planes per 32-row tile:
+// plane0 = dwords 0-3 (16 B per row), plane1 = dwords 4-5 (8 B per row).
+__device__ __forceinline__ uint32_t e3m2_code(int v) {
+  const uint32_t a = static_cast<uint32_t>(v < 0 ? -v : v);
+  const int e = 31 - __builtin_clz(a | 1u);  // floor(log2 a) for a >= 1
+  const uint32_t mag = ((static_cast<uint32_t>(e) + 3u) << 2) | (((a << 2) >> e) & 3u);
+  return a == 0 ? 0u : ((v < 0 ? 0x20u : 0u) | mag);
+}
+
+__device__ __forceinline__ void split_h_l(int q, int &h, int &l) {
+  h = (q + 8) >> 4;  // arithmetic shift: floor((q + 8) / 16)
+  l = q - 16 * h;
+}
+
+// Dense packing across the 8 lanes of a 32-element block (lane g holds 4
+// codes = 24 bits v_g): the 6 dwords of the block are, per quad of lanes,
+// dword 3q + r = (v_r >> 8r) | (v_{r+1} << (24 - 8r)) for r = 0, 1, 2.
+// Returns that dword in lanes with r < 3 (lane r of each quad); lane 3's
+// return value is meaningless.  quad_perm [1,2,3,3] fetches v_{r+1}.
+__device__ __forceinline__ uint32_t pack24_group8(uint32_t v) {
+  const uint32_t nxt =
+      static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xF9, 0xf, 0xf, false));
+  const int r = threadIdx.x & 3;
+  return (v >> (8 * r)) | (nxt << (24 - 8 * r));
+}
+
+// Four int8 codes (packed bytes) -> 24-bit E3M2 streams of their h and l parts.
+__device__ __forceinline__ void codes24_hl(int q4packed, uint32_t &vh, uint32_t &vl) {
+  vh = 0;
+  vl = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int h, l;
+    split_h_l(static_cast<int8_t>(q4packed >> (8 * i)), h, l);
+    vh |= e3m2_code(h) << (6 * i);
+    vl |= e3m2_code(l) << (6 * i);
+  }
+}
+
+// Byte offset of dword d (0..5) of operand row `row` within a 768-byte
+// (plane0 | plane1) tile image.
+__device__ __forceinline__ uint32_t mx_dword_off(int row, int d) {
+  return d < 4 ? static_cast<uint32_t>(row * 16 + d * 4) : static_cast<uint32_t>(512 + row * 8 + (d - 4) * 4);
+}
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+// Read one MFMA operand row (6 dwords) from a 768-byte tile image (LDS or global).
+__device__ __forceinline__ v8i mx_row(const char *tile, int row) {
+  const uint4 p0 = *reinterpret_cast<const uint4 *>(tile + row * 16);
+  const uint2 p1 = *reinterpret_cast<const uint2 *>(tile + 512 + row * 8);
+  v8i r;
+  r[0] = static_cast<int>(p0.x);
+  r[1] = static_cast<int>(p0.y);
+  r[2] = static_cast<int>(p0.z);
+  r[3] = static_cast<int>(p0.w);
+  r[4] = static_cast<int>(p1.x);
+  r[5] = static_cast<int>(p1.y);
+  r[6] = 0;
+  r[7] = 0;
+  return r;
+}
+
+// Exact integer block dots of a 32 (weight rows) x 32 (tokens) tile for one
+// 32-element block, as f32: D[i][j] = sum_k w[i][k] * q[j][k].
+// A = [w | w] (K = 64, lanes 0-31 and 32-63 hold the same weight row), B =
+// [h | l] (lanes 0-31 hold token j's h codes, lanes 32-63 its l codes) with
+// E8M0 scale 2^4 on the h half: sum_k w*(16h) + sum_k w*l = sum_k w*q.
+// Products and partial sums are integers below 2^24, so D is exact.
+// Output layout: lane L, element v -> j = L % 32, i = 8*(v/4) + 4*(L/32) + v%4.
+__device__ __forceinline__ v16f mx_block_dot(v8i a, v8i b) {
+  const v16f zero = {};
+  const int scale_b = (threadIdx.x & 32) ? 127 : 131;  // 2^0 on l, 2^4 on h
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, zero, 3, 3, 0, 127, 0, scale_b);
+}
+
 }  // namespace lgh

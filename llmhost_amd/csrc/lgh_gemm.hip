@@ -1,19 +1,28 @@
-// M > 1 kernels for gfx950: Q4 x int8 GEMM on v_mfma_i32_32x32x32_i8 with a
-// per-32-block scale fold (replaces crates/llm-cpu/src/gemv_q4.rs:686-952 and
-// the AMX tiles of crates/llm-cpu/src/amx.rs:329-518).
+// M > 1 kernels for gfx950: the Q4 x ActQ8 GEMM (replaces
+// crates/llm-cpu/src/gemv_q4.rs:686-952 and the AMX tiles of
+// crates/llm-cpu/src/amx.rs:329-518).
 //
-// One 32-element K block is exactly one MFMA K step, so each MFMA yields the
-// exact integer block dots of a 32x32 (weight rows n) x (tokens m) tile --
-// the analogue of amx.rs's tdpbssd + tilestored -- and the fold
-//   acc[n][m] = fma(f32(16*c), sw[n,kb] * sa[m,kb], acc[n][m])
-// is the analogue of fold_c (amx.rs:263-320).  A operand = unpacked weight
-// nibbles (16 x value, see lgh_internal.h), B operand = quantized activations;
-// the x16 is removed once at the store.
+// Per 32-element block the reference computes the exact integer dot of a
+// weight row and a token, then folds it in f32:
+//   acc[n][m] = fma(f32(dot), sw[n,kb] * sa[m,kb], acc[n][m])   (gemv_q4.rs:930-936)
+// On the matrix cores this becomes, for a 32 x 32 (rows x tokens) tile:
+//   * the block dots: one scaled fp6 MFMA (mx_block_dot, lgh_device.h) whose
+//     f32 result is the exact integer dot -- the analogue of tdpbssd +
+//     tilestored (amx.rs:329-380), with no int->float conversion;
+//   * the scale products sw[n] * sa[m] of two consecutive blocks: one f32
+//     32x32x1_2b MFMA outer product, laid out exactly like the block dots
+//     (block b in elements 16b..16b+15);
+//   * the fold: one v_fma_f32 per element and block -- the only VALU work of
+//     the inner loop (fold_c, amx.rs:263-320).
+// (With int8 MFMA the fold costs a convert, a multiply and an FMA per
+// element: three VALU ops per 32-deep MFMA result, which caps the GEMM near
+// one sixth of the int8 matrix peak.  Here it is one.)
 //
-// Workgroup = 4 waves in a WN x WM grid; each wave owns TN x TM MFMA tiles.
-// K is staged through LDS in chunks of KC blocks with a register prefetch of
-// the next chunk.  LDS planes are [block q][half h][row][bytes] so every MFMA
-// operand read is a contiguous, conflict-free ds_read.
+// Workgroup = 4 waves in a WN x WM grid, each owning TN x TM 32x32 tiles.
+// K advances one block pair per stage.  A stage is the verbatim concatenation
+// of NS weight records and MS activation records (lgh_internal.h), copied by
+// 16-byte chunks through registers into one of two LDS buffers; the copy of
+// stage p+1 is in flight while stage p is computed, one barrier per stage.
 #include "lgh_device.h"
 #include "lgh_internal.h"
 
@@ -22,144 +31,155 @@ namespace lgh {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int KC = 4;  // K blocks per LDS chunk
+constexpr int kWRec = static_cast<int>(kMxWRec);
+constexpr int kARec = static_cast<int>(kMxARec);
+constexpr int kTile = static_cast<int>(kMxTile);
+constexpr long kSplitTarget = 256;  // workgroups worth filling the chip with (one per CU)
 
 struct GemmArgs {
-  const uint8_t *qs;   // weights: [n][bpr][16]
-  const uint16_t *sc;  // [n][bpr]
-  const int8_t *aq;    // activations: [m][k]
-  const float *sa;     // [m][bpr]
+  const uint8_t *wmx;  // weight operand image [nt][pp]
+  const uint8_t *amx;  // activation operand image [mt][pp]
   float *y;            // [m][n]
-  int n, m, k, bpr, mode;
+  float *part;         // split-K partials [splits][m][n] (splits > 1)
+  int n, m, nt, mt, pp, mode, vec4, splits;
+  uint32_t w_bytes, a_bytes;
 };
 
 template <int WN, int WM, int TN, int TM>
 struct Cfg {
-  static constexpr int BN = WN * TN * 32;
-  static constexpr int BM = WM * TM * 32;
-  // LDS plane strides (bytes), padded by 16 so the 2*KC planes start on
-  // different banks for the staging writes.
-  static constexpr int W_PLANE = BN * 8 + 16;
-  static constexpr int A_PLANE = BM * 16 + 16;
-  static constexpr int W_BYTES = KC * 2 * W_PLANE;
-  static constexpr int A_BYTES = KC * 2 * A_PLANE;
-  static constexpr int SW_BYTES = KC * BN * 4;
-  static constexpr int SA_BYTES = KC * BM * 4;
-  static constexpr int LDS = W_BYTES + A_BYTES + SW_BYTES + SA_BYTES;
-  // Per-thread staging counts.
-  static constexpr int W_LD = (BN * KC + kThreads - 1) / kThreads;      // uint4 blocks
-  static constexpr int A_LD = (BM * KC * 2 + kThreads - 1) / kThreads;  // uint4 halves
-  static constexpr int SW_LD = (BN * KC + kThreads - 1) / kThreads;
-  static constexpr int SA_LD = (BM * KC + kThreads - 1) / kThreads;
+  static constexpr int NS = WN * TN;  // 32-row weight tiles per workgroup
+  static constexpr int MS = WM * TM;  // 32-token tiles per workgroup
+  static constexpr int W_CH = NS * kWRec / 16;
+  static constexpr int A_CH = MS * kARec / 16;
+  static constexpr int W_LD = (W_CH + kThreads - 1) / kThreads;
+  static constexpr int A_LD = (A_CH + kThreads - 1) / kThreads;
+  // Each region is padded to whole 256-chunk slots so every thread stores
+  // every slot without a branch (the padding receives zeros).
+  static constexpr int A_LDS = W_LD * kThreads * 16;  // activation records start here in a stage
+  static constexpr int STAGE = A_LDS + A_LD * kThreads * 16;
+  static constexpr int LDS = 2 * STAGE;
   static_assert(WN * WM * 64 == kThreads, "4 waves per workgroup");
+  static_assert(kWRec % 16 == 0 && kARec % 16 == 0, "records are 16-byte chunks");
 };
 
 template <class C>
 struct Stage {
   uint4 w[C::W_LD];
   uint4 a[C::A_LD];
-  uint16_t sw[C::SW_LD];  // f16 bits; converted when written to LDS
-  float sa[C::SA_LD];
 };
 
-// Issue every global load of one K chunk, all branch-free raw buffer loads.
-// The resources cover this workgroup's operand panels: rows beyond n / m fall
-// outside them and load as 0; blocks beyond bpr get kOOB offsets.  They are
-// rebuilt from scalars here (kernel arguments and blockIdx) so the compiler
-// keeps them in SGPRs.
+// Byte offsets (stage 0) of this thread's chunks in the two images; kOOB for
+// slots past the stage.  Tiles past nt / mt land past the image end and load
+// as zeros through the buffer range check.
 template <class C>
-__device__ __forceinline__ void load_chunk(const GemmArgs &g, int n0, int m0, int kb0, Stage<C> &s) {
+struct Slots {
+  uint32_t w[C::W_LD];
+  uint32_t a[C::A_LD];
+};
+
+template <class C>
+__device__ __forceinline__ void init_slots(const GemmArgs &g, int nt0, int mt0, Slots<C> &s) {
   const int tid = threadIdx.x;
-  // readfirstlane: the clamps select to VALU med3, which would otherwise put
-  // the resource sizes in VGPRs (and every load in a waterfall loop).
-  const uint32_t rn = static_cast<uint32_t>(uniform(max(0, min(C::BN, g.n - n0))));
-  const uint32_t rm = static_cast<uint32_t>(uniform(max(0, min(C::BM, g.m - m0))));
-  const size_t wb = static_cast<size_t>(n0) * g.bpr, ab = static_cast<size_t>(m0);
-  const auto pw = make_rsrc(g.qs + wb * 16, rn * g.bpr * 16u);
-  const auto psw = make_rsrc(g.sc + wb, rn * g.bpr * 2u);
-  const auto pa = make_rsrc(g.aq + ab * g.k, rm * static_cast<uint32_t>(g.k));
-  const auto psa = make_rsrc(g.sa + ab * g.bpr, rm * g.bpr * 4u);
 #pragma unroll
   for (int i = 0; i < C::W_LD; i++) {
-    const int c = tid + i * kThreads;  // c -> (row, q): 4 threads cover a row's 64 B
-    const int row = c / KC, kb = kb0 + c % KC;
-    const bool ok = c < C::BN * KC && kb < g.bpr;
-    s.w[i] = buf_load16<kAuxNT>(pw, ok ? static_cast<uint32_t>(row * g.bpr + kb) * 16u : kOOB);
-  }
-#pragma unroll
-  for (int i = 0; i < C::SW_LD; i++) {
     const int c = tid + i * kThreads;
-    const int row = c / KC, kb = kb0 + c % KC;
-    const bool ok = c < C::BN * KC && kb < g.bpr;
-    s.sw[i] = buf_load_u16(psw, ok ? static_cast<uint32_t>(row * g.bpr + kb) * 2u : kOOB);
+    const int t = c / (kWRec / 16), off = (c % (kWRec / 16)) * 16;
+    s.w[i] = c < C::W_CH ? static_cast<uint32_t>((nt0 + t) * g.pp) * kWRec + off : kOOB;
   }
 #pragma unroll
   for (int i = 0; i < C::A_LD; i++) {
-    const int c = tid + i * kThreads;  // c -> (row, q, h): 8 threads cover a row's 128 B
-    const int row = c / (KC * 2), qh = c % (KC * 2);
-    const bool ok = c < C::BM * KC * 2 && kb0 + qh / 2 < g.bpr;
-    s.a[i] = buf_load16(pa, ok ? static_cast<uint32_t>(row * g.k + kb0 * 32 + qh * 16) : kOOB);
-  }
-#pragma unroll
-  for (int i = 0; i < C::SA_LD; i++) {
     const int c = tid + i * kThreads;
-    const int row = c / KC, kb = kb0 + c % KC;
-    const bool ok = c < C::BM * KC && kb < g.bpr;
-    s.sa[i] = buf_load_f32(psa, ok ? static_cast<uint32_t>(row * g.bpr + kb) * 4u : kOOB);
+    const int t = c / (kARec / 16), off = (c % (kARec / 16)) * 16;
+    s.a[i] = c < C::A_CH ? static_cast<uint32_t>((mt0 + t) * g.pp) * kARec + off : kOOB;
   }
 }
 
+// Stage p >= pend (prefetches issued during the last stages) loads zeros.
 template <class C>
-__device__ __forceinline__ void store_chunk(char *lds, const Stage<C> &s) {
+__device__ __forceinline__ void load_stage(const GemmArgs &g, const Slots<C> &s, int p, int pend, Stage<C> &st) {
+  const auto rw = make_rsrc(g.wmx, g.w_bytes);
+  const auto ra = make_rsrc(g.amx, g.a_bytes);
+  const bool live = p < pend;
+  const uint32_t dw = static_cast<uint32_t>(p) * kWRec, da = static_cast<uint32_t>(p) * kARec;
+#pragma unroll
+  for (int i = 0; i < C::W_LD; i++) st.w[i] = buf_load16(rw, (s.w[i] == kOOB || !live) ? kOOB : s.w[i] + dw);
+#pragma unroll
+  for (int i = 0; i < C::A_LD; i++) st.a[i] = buf_load16(ra, (s.a[i] == kOOB || !live) ? kOOB : s.a[i] + da);
+}
+
+template <class C>
+__device__ __forceinline__ void store_stage(char *buf, const Stage<C> &st) {
   const int tid = threadIdx.x;
-  char *s_w = lds;
-  char *s_a = lds + C::W_BYTES;
-  float *s_sw = reinterpret_cast<float *>(lds + C::W_BYTES + C::A_BYTES);
-  float *s_sa = s_sw + KC * C::BN;
 #pragma unroll
-  for (int i = 0; i < C::W_LD; i++) {
-    const int c = tid + i * kThreads;
-    if (c < C::BN * KC) {
-      const int row = c / KC, q = c % KC;
-      *reinterpret_cast<uint2 *>(s_w + (2 * q) * C::W_PLANE + row * 8) = make_uint2(s.w[i].x, s.w[i].y);
-      *reinterpret_cast<uint2 *>(s_w + (2 * q + 1) * C::W_PLANE + row * 8) = make_uint2(s.w[i].z, s.w[i].w);
+  for (int i = 0; i < C::W_LD; i++) *reinterpret_cast<uint4 *>(buf + (tid + i * kThreads) * 16) = st.w[i];
+#pragma unroll
+  for (int i = 0; i < C::A_LD; i++) *reinterpret_cast<uint4 *>(buf + C::A_LDS + (tid + i * kThreads) * 16) = st.a[i];
+}
+
+// One stage of the inner loop for a wave's TN x TM tiles: per tile, the
+// outer product of the two blocks' scales, the two blocks' exact dots, and
+// 32 FMAs folding them into the accumulators (block order as in the reference).
+template <class C, int TN, int TM>
+__device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, float (&acc)[TN][TM][16]) {
+  const int lane = threadIdx.x & 63, row = lane & 31, half = lane >> 5;
+  const v32f zero32 = {};
+  // Scale inputs of the outer products: lane L holds block L/32, row or token
+  // L%32 -- the record's f32 scale array [block][row] read linearly.
+  float xs[TN], ys[TM];
+  v8i A[2][TN], B[2][TM];
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++) {
+    const char *rec = buf + (wn * TN + tn) * kWRec;
+    xs[tn] = reinterpret_cast<const float *>(rec + 2 * kTile)[lane];
+    A[0][tn] = mx_row(rec, row);
+    A[1][tn] = mx_row(rec + kTile, row);
+  }
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++) {
+    const char *rec = buf + C::A_LDS + (wm * TM + tm) * kARec;
+    ys[tm] = reinterpret_cast<const float *>(rec + 4 * kTile)[lane];
+    B[0][tm] = mx_row(rec + half * kTile, row);
+    B[1][tm] = mx_row(rec + (2 + half) * kTile, row);
+  }
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) {
+      const v32f P = __builtin_amdgcn_mfma_f32_32x32x1f32(xs[tn], ys[tm], zero32, 0, 0, 0);
+      const v16f c0 = mx_block_dot(A[0][tn], B[0][tm]);
+      const v16f c1 = mx_block_dot(A[1][tn], B[1][tm]);
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c0[v], P[v], acc[tn][tm][v]);
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c1[v], P[16 + v], acc[tn][tm][v]);
     }
-  }
-#pragma unroll
-  for (int i = 0; i < C::SW_LD; i++) {
-    const int c = tid + i * kThreads;
-    if (c < C::BN * KC) s_sw[(c % KC) * C::BN + c / KC] = h2f(s.sw[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < C::A_LD; i++) {
-    const int c = tid + i * kThreads;
-    if (c < C::BM * KC * 2) {
-      const int row = c / (KC * 2), qh = c % (KC * 2);
-      *reinterpret_cast<uint4 *>(s_a + qh * C::A_PLANE + row * 16) = s.a[i];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < C::SA_LD; i++) {
-    const int c = tid + i * kThreads;
-    if (c < C::BM * KC) s_sa[(c % KC) * C::BM + c / KC] = s.sa[i];
-  }
+}
+
+// Stage p: `spent` held stage p (already in LDS) and is refilled with stage
+// p+2; `next` holds stage p+1 and goes to the other LDS buffer after the
+// compute.  The sched_barrier keeps that store -- and its wait for the
+// global loads -- behind the MFMAs and folds.
+// LDS buffer (p - p0) & 1 holds stage p.
+template <class C, int TN, int TM>
+__device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int p, int p0, int pend,
+                                              char *lds, int wn, int wm, float (&acc)[TN][TM][16], Stage<C> &spent,
+                                              Stage<C> &next) {
+  load_stage<C>(g, slots, p + 2, pend, spent);
+  compute_stage<C, TN, TM>(lds + ((p - p0) & 1) * C::STAGE, wn, wm, acc);
+  __builtin_amdgcn_sched_barrier(0);
+  store_stage<C>(lds + ((p - p0 + 1) & 1) * C::STAGE, next);
+  __syncthreads();
 }
 
 template <int WN, int WM, int TN, int TM>
-__global__ __launch_bounds__(kThreads) void q4_gemm_mfma_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
   using C = Cfg<WN, WM, TN, TM>;
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
   const int wn = wave % WN, wm = wave / WN;
-  const int col = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * C::BN;
-  const int m0 = blockIdx.y * C::BM;
-
-  const char *s_w = lds;
-  const char *s_a = lds + C::W_BYTES;
-  const float *s_sw = reinterpret_cast<const float *>(lds + C::W_BYTES + C::A_BYTES);
-  const float *s_sa = s_sw + KC * C::BN;
+  const int row = lane & 31, half = lane >> 5;
+  const int nt0 = blockIdx.x * C::NS, mt0 = blockIdx.y * C::MS;
 
   float acc[TN][TM][16];
 #pragma unroll
@@ -169,133 +189,167 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; v++) acc[tn][tm][v] = 0.0f;
 
-  const int nchunks = (g.bpr + KC - 1) / KC;
-  Stage<C> st;
-  load_chunk<C>(g, n0, m0, 0, st);
-  store_chunk<C>(lds, st);
+  Slots<C> slots;
+  init_slots<C>(g, nt0, mt0, slots);
+  // Two register stages in flight: while stage p is computed from LDS, stage
+  // p+1 waits in registers for its LDS store and stage p+2 is being fetched.
+  // Split z of the K range: block pairs [p0, pend).
+  const int z = blockIdx.z;
+  const int p0 = static_cast<int>(static_cast<long>(g.pp) * z / g.splits);
+  const int pend = static_cast<int>(static_cast<long>(g.pp) * (z + 1) / g.splits);
+  Stage<C> s0, s1;
+  load_stage<C>(g, slots, p0, pend, s0);
+  load_stage<C>(g, slots, p0 + 1, pend, s1);
+  store_stage<C>(lds, s0);
   __syncthreads();
 
-  for (int ch = 0; ch < nchunks; ch++) {
-    if (ch + 1 < nchunks) load_chunk<C>(g, n0, m0, (ch + 1) * KC, st);
-    // Not unrolled: unrolling lets the scheduler hoist all KC*TN*TM MFMAs and
-    // keep their 16-register results live at once (register spills).
-#pragma unroll 1
-    for (int q = 0; q < KC; q++) {
-      v4i A[TN], B[TM];
-#pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        const int nl = (wn * TN + tn) * 32 + col;
-        A[tn] = unpack_half16(*reinterpret_cast<const uint2 *>(s_w + (2 * q + h) * C::W_PLANE + nl * 8));
-      }
-#pragma unroll
-      for (int tm = 0; tm < TM; tm++) {
-        const int ml = (wm * TM + tm) * 32 + col;
-        B[tm] = *reinterpret_cast<const v4i *>(s_a + (2 * q + h) * C::A_PLANE + ml * 16);
-      }
-      float sa[TM];
-#pragma unroll
-      for (int tm = 0; tm < TM; tm++) sa[tm] = s_sa[q * C::BM + (wm * TM + tm) * 32 + col];
-#pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        float sw[16];
-#pragma unroll
-        for (int gq = 0; gq < 4; gq++) {
-          const float4 f = *reinterpret_cast<const float4 *>(s_sw + q * C::BN + (wn * TN + tn) * 32 + 8 * gq + 4 * h);
-          sw[4 * gq + 0] = f.x;
-          sw[4 * gq + 1] = f.y;
-          sw[4 * gq + 2] = f.z;
-          sw[4 * gq + 3] = f.w;
-        }
-#pragma unroll
-        for (int tm = 0; tm < TM; tm++) {
-          const v16i zero = {};
-          const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[tn], B[tm], zero, 0, 0, 0);
-#pragma unroll
-          for (int v = 0; v < 16; v++)
-            acc[tn][tm][v] = fmaf(static_cast<float>(c[v]), sw[v] * sa[tm], acc[tn][tm][v]);
-        }
-      }
-    }
-    __syncthreads();
-    if (ch + 1 < nchunks) {
-      store_chunk<C>(lds, st);
-      __syncthreads();
-    }
+  int p = p0;
+  for (; p + 1 < pend; p += 2) {
+    pipeline_step<C, TN, TM>(g, slots, p, p0, pend, lds, wn, wm, acc, s0, s1);
+    pipeline_step<C, TN, TM>(g, slots, p + 1, p0, pend, lds, wn, wm, acc, s1, s0);
   }
+  if (p < pend) pipeline_step<C, TN, TM>(g, slots, p, p0, pend, lds, wn, wm, acc, s0, s1);
 
-  // D[i][j] of a 32x32 MFMA tile: lane l, element v -> j = l % 32,
-  // i = 8*(v/4) + 4*(l/32) + v%4.  Here i = weight row n, j = token m.
+  // With split K the partial sums go to part[z] (assign); a second kernel
+  // adds the splits in order and applies the caller's mode.
+  const bool split = g.splits > 1;
+  float *const out = split ? g.part + static_cast<size_t>(z) * g.m * g.n : g.y;
+  const int mode = split ? LGH_ASSIGN : g.mode;
+  const bool vec4 = split ? (g.n % 4 == 0) : (g.vec4 != 0);
+
+  // Element v of a lane: token j = L % 32, weight row i = 8*(v/4) + 4*(L/32) + v%4,
+  // so each group of 4 elements is 4 consecutive outputs of one token.
 #pragma unroll
   for (int tn = 0; tn < TN; tn++)
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
-      const int m = m0 + (wm * TM + tm) * 32 + col;
-      if (m >= g.m) continue;
-      float *yrow = g.y + static_cast<size_t>(m) * g.n;
+      const int j = (mt0 + wm * TM + tm) * 32 + row;
+      if (j >= g.m) continue;
+      float *yrow = out + static_cast<size_t>(j) * g.n;
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int n = n0 + (wn * TN + tn) * 32 + 8 * (v / 4) + 4 * h + (v % 4);
-        if (n < g.n) {
-          const float val = acc[tn][tm][v] * 0.0625f;
-          if (g.mode == LGH_ADD_F64)
-            yrow[n] = static_cast<float>(static_cast<double>(yrow[n]) + static_cast<double>(val));
-          else
-            yrow[n] = val;
+      for (int q = 0; q < 4; q++) {
+        const int i0 = (nt0 + wn * TN + tn) * 32 + 8 * q + 4 * half;
+        float v[4] = {acc[tn][tm][4 * q], acc[tn][tm][4 * q + 1], acc[tn][tm][4 * q + 2], acc[tn][tm][4 * q + 3]};
+        if (vec4 && i0 + 3 < g.n) {
+          float4 *dst = reinterpret_cast<float4 *>(yrow + i0);
+          if (mode == LGH_ADD_F64) {
+            const float4 o = *dst;
+            v[0] = static_cast<float>(static_cast<double>(o.x) + static_cast<double>(v[0]));
+            v[1] = static_cast<float>(static_cast<double>(o.y) + static_cast<double>(v[1]));
+            v[2] = static_cast<float>(static_cast<double>(o.z) + static_cast<double>(v[2]));
+            v[3] = static_cast<float>(static_cast<double>(o.w) + static_cast<double>(v[3]));
+          }
+          *dst = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            if (i0 + e >= g.n) continue;
+            if (mode == LGH_ADD_F64)
+              yrow[i0 + e] = static_cast<float>(static_cast<double>(yrow[i0 + e]) + static_cast<double>(v[e]));
+            else
+              yrow[i0 + e] = v[e];
+          }
         }
       }
     }
 }
 
-// Integer block dots through the MFMA operand path: one wave per
-// (32 weight rows, 32 tokens, block kb); out[m][n][kb] = c / 16.
-__global__ __launch_bounds__(64) void q4_mfma_block_dots_kernel(const uint8_t *__restrict__ qs,
-                                                                const int8_t *__restrict__ aq, int n,
-                                                                int m, int k, int bpr, int32_t *out) {
-  const int lane = threadIdx.x, col = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32, kb = blockIdx.z;
-  const int nr = n0 + col, mr = m0 + col;
-  uint2 w = make_uint2(0, 0);
-  if (nr < n) w = *reinterpret_cast<const uint2 *>(qs + (static_cast<size_t>(nr) * bpr + kb) * 16 + 8 * h);
-  v4i b = {0, 0, 0, 0};
-  if (mr < m) b = *reinterpret_cast<const v4i *>(aq + static_cast<size_t>(mr) * k + kb * 32 + 16 * h);
-  const v16i zero = {};
-  const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_half16(w), b, zero, 0, 0, 0);
+// Exact block dots through the same operand images and MFMA: one wave per
+// (32-row tile, 32-token tile, block kb); out[m][n][kb] = dot.
+__global__ __launch_bounds__(64) void q4_mx_block_dots_kernel(const uint8_t *__restrict__ wmx,
+                                                              const uint8_t *__restrict__ amx, int n, int m,
+                                                              int bpr, int pp, int32_t *out) {
+  const int lane = threadIdx.x, row = lane & 31, half = lane >> 5;
+  const int t = blockIdx.x, u = blockIdx.y, kb = blockIdx.z;
+  const char *wrec = reinterpret_cast<const char *>(wmx) + (static_cast<size_t>(t) * pp + kb / 2) * kMxWRec;
+  const char *arec = reinterpret_cast<const char *>(amx) + (static_cast<size_t>(u) * pp + kb / 2) * kMxARec;
+  const v8i a = mx_row(wrec + (kb & 1) * kTile, row);
+  const v8i b = mx_row(arec + (2 * (kb & 1) + half) * kTile, row);
+  const v16f c = mx_block_dot(a, b);
   for (int v = 0; v < 16; v++) {
-    const int i = n0 + 8 * (v / 4) + 4 * h + (v % 4);
-    const int j = m0 + col;
-    if (i < n && j < m) out[(static_cast<size_t>(j) * n + i) * bpr + kb] = c[v] >> 4;
+    const int i = t * 32 + 8 * (v / 4) + 4 * half + (v % 4);
+    const int j = u * 32 + row;
+    if (i < n && j < m) out[(static_cast<size_t>(j) * n + i) * bpr + kb] = static_cast<int32_t>(c[v]);
   }
 }
 
+// y = sum over splits of part[z] (z ascending), then the caller's mode.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int splits,
+                                                            size_t total, float *y, int mode) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  float v = part[i];
+  for (int z = 1; z < splits; z++) v += part[static_cast<size_t>(z) * total + i];
+  y[i] = mode == LGH_ADD_F64 ? static_cast<float>(static_cast<double>(y[i]) + static_cast<double>(v)) : v;
+}
+
 template <int WN, int WM, int TN, int TM>
-hipError_t launch_cfg(const GemmArgs &g, hipStream_t st) {
+int splits_for(size_t nt, size_t mt, size_t pp) {
   using C = Cfg<WN, WM, TN, TM>;
-  const dim3 grid((g.n + C::BN - 1) / C::BN, (g.m + C::BM - 1) / C::BM);
-  hipLaunchKernelGGL((q4_gemm_mfma_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), C::LDS, st, g);
+  const long tiles = static_cast<long>((nt + C::NS - 1) / C::NS) * static_cast<long>((mt + C::MS - 1) / C::MS);
+  // Split K when the tiles alone leave CUs idle: aim for >= kSplitTarget
+  // workgroups while keeping >= 8 block pairs per split.
+  int splits = 1;
+  while (tiles * splits < kSplitTarget && pp / (2 * splits) >= 8) splits *= 2;
+  return splits;
+}
+
+template <int WN, int WM, int TN, int TM>
+hipError_t launch_cfg(GemmArgs g, int splits, float *part, hipStream_t st) {
+  using C = Cfg<WN, WM, TN, TM>;
+  const size_t mn = static_cast<size_t>(g.m) * g.n;
+  g.splits = splits;
+  g.part = part;
+  const dim3 grid((g.nt + C::NS - 1) / C::NS, (g.mt + C::MS - 1) / C::MS, splits);
+  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), C::LDS, st, g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, st, part,
+                     splits, mn, g.y, g.mode);
   return hipGetLastError();
 }
 
-inline long tiles(long n, long m, int bn, int bm) { return ((n + bn - 1) / bn) * ((m + bm - 1) / bm); }
-
 }  // namespace
 
-hipError_t launch_q4_gemm(const lgh_q4 *w, const int8_t *aq, const float *sa, float *y, size_t m, int mode,
-                          hipStream_t st) {
-  GemmArgs g{w->qs, w->sc, aq, sa, y, static_cast<int>(w->n), static_cast<int>(m), static_cast<int>(w->k),
-             static_cast<int>(w->bpr), mode};
-  if (g.n == 0 || g.m == 0) return hipSuccess;
-  if (m <= 32) return launch_cfg<4, 1, 1, 1>(g, st);  // 128 n x 32 m
-  if (tiles(g.n, g.m, 128, 128) >= 240) return launch_cfg<2, 2, 2, 2>(g, st);
-  return launch_cfg<2, 2, 1, 1>(g, st);  // 64 x 64
+int plan_q4_gemm_splits(const lgh_q4 *w, size_t m) {
+  const size_t mt = (m + 31) / 32;
+  if (m <= 32) return splits_for<4, 1, 1, 1>(w->nt, mt, w->pp);
+  if (m <= 64) return splits_for<4, 1, 1, 2>(w->nt, mt, w->pp);
+  return splits_for<2, 2, 2, 2>(w->nt, mt, w->pp);
 }
 
-hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const int8_t *aq, size_t m, int32_t *out,
+hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t m, int mode, float *part,
+                          size_t part_floats, hipStream_t st) {
+  if (w->n == 0 || m == 0) return hipSuccess;
+  int splits = plan_q4_gemm_splits(w, m);
+  while (splits > 1 && static_cast<size_t>(splits) * m * w->n > part_floats) splits /= 2;
+  const size_t mt = (m + 31) / 32;
+  GemmArgs g{w->mx,
+             mxa,
+             y,
+             nullptr,
+             static_cast<int>(w->n),
+             static_cast<int>(m),
+             static_cast<int>(w->nt),
+             static_cast<int>(mt),
+             static_cast<int>(w->pp),
+             mode,
+             (w->n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0) ? 1 : 0,
+             1,
+             static_cast<uint32_t>(w->nt * w->pp * kMxWRec),
+             static_cast<uint32_t>(mt * w->pp * kMxARec)};
+  if (m <= 32) return launch_cfg<4, 1, 1, 1>(g, splits, part, st);  // 128 rows x 32 tokens
+  if (m <= 64) return launch_cfg<4, 1, 1, 2>(g, splits, part, st);  // 128 x 64
+  return launch_cfg<2, 2, 2, 2>(g, splits, part, st);               // 128 x 128
+}
+
+hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const uint8_t *mxa, size_t m, int32_t *out,
                                      hipStream_t st) {
   if (w->n == 0 || m == 0 || w->bpr == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((w->n + 31) / 32), static_cast<unsigned>((m + 31) / 32),
+  const dim3 grid(static_cast<unsigned>(w->nt), static_cast<unsigned>((m + 31) / 32),
                   static_cast<unsigned>(w->bpr));
-  hipLaunchKernelGGL(q4_mfma_block_dots_kernel, grid, dim3(64), 0, st, w->qs, aq, static_cast<int>(w->n),
-                     static_cast<int>(m), static_cast<int>(w->k), static_cast<int>(w->bpr), out);
+  hipLaunchKernelGGL(q4_mx_block_dots_kernel, grid, dim3(64), 0, st, w->mx, mxa, static_cast<int>(w->n),
+                     static_cast<int>(m), static_cast<int>(w->bpr), static_cast<int>(w->pp), out);
   return hipGetLastError();
 }
 

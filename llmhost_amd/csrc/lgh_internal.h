@@ -14,6 +14,20 @@
 // The factor 16 is exact and is removed once per output (x 1/16).
 //
 // Q8_0 matrix: qs plane int8 [n][bpr][32] (natural order) + sc plane f16.
+//
+// GEMM operand images (M > 1 path, fp6 matrix cores; codes defined in
+// lgh_device.h).  Rows are grouped in 32-row tiles, blocks in pairs; every
+// (tile, pair) record is one contiguous chunk that the GEMM copies verbatim
+// into LDS:
+//   weights     mx plane: [nt = ceil(n/32)][pp = ceil(bpr/2)] records of
+//               kMxWRec bytes = 2 blocks x 768-byte code tile, then the 64 f32
+//               block scales [block][row];
+//   activations (per call, in the context workspace): [mt = ceil(m/32)][pp]
+//               records of kMxARec bytes = 2 blocks x {h, l} x 768-byte code
+//               tile, then 64 f32 block scales [block][token].
+// A 768-byte code tile is plane0 (32 rows x 16 B: dwords 0-3 of each row)
+// followed by plane1 (32 rows x 8 B: dwords 4-5).  Rows past n / m and blocks
+// past bpr are zero codes with zero scales.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -31,7 +45,7 @@ struct lgh_ctx {
   hipStream_t stream = nullptr;
   int act_mode = LGH_ACT_PER_BLOCK;
   std::string err;
-  // GEMM activation workspace: int8 qs [m][k] + f32 scales [m][k/32] + f32 row scales [m].
+  // GEMM workspace: activation operand image, f32 row scales [m], split-K partials.
   void *ws = nullptr;
   size_t ws_bytes = 0;
   // Device staging for the host-pointer entry points.
@@ -44,6 +58,8 @@ struct lgh_q4 {
   size_t n = 0, k = 0, bpr = 0;
   uint8_t *qs = nullptr;   // n*bpr*16 bytes
   uint16_t *sc = nullptr;  // n*bpr halves (same allocation as qs)
+  uint8_t *mx = nullptr;   // GEMM operand image: nt*pp*kMxWRec bytes (own allocation)
+  size_t nt = 0, pp = 0;
 };
 
 struct lgh_q8 {
@@ -56,6 +72,21 @@ struct lgh_q8 {
 // ---- internal launchers (return hipError_t of the launch) ----------------
 // All enqueue on `stream`; all pointers are device pointers.
 namespace lgh {
+
+constexpr size_t kMxTile = 768;                 // one 32-row x 32-code tile
+constexpr size_t kMxWRec = 2 * kMxTile + 256;   // weights: 2 tiles + 64 f32 scales
+constexpr size_t kMxARec = 4 * kMxTile + 256;   // activations: 2 x {h, l} tiles + 64 f32
+// Buffer-load offsets are 32-bit: operand images must stay below this.
+constexpr size_t kMxMaxBytes = size_t(1) << 31;
+
+// Weight operand image from the repacked nibble/scale planes (load time).
+hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t stream);
+// Activation operand image: quantize x[m][k] per ActQ8 (per_row selects the
+// mode; row_scale is scratch for m floats) straight into mt*pp records.
+hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, uint8_t *mxa,
+                               float *row_scale, hipStream_t stream);
+// Same record layout from already-quantized int8 activations (scales left 0).
+hipError_t launch_act_split_mx(const int8_t *aq, size_t m, size_t k, uint8_t *mxa, hipStream_t stream);
 
 hipError_t launch_q4_repack(const uint8_t *raw_blocks, size_t nblocks, uint8_t *qs, uint16_t *sc,
                             hipStream_t stream);
@@ -90,16 +121,22 @@ hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t toke
 hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int8_t *qs,
                             float *scales, int32_t *sums, float *row_scale, hipStream_t stream);
 
-// GEMM on pre-quantized activations: y[m][n] (+)= aq[m][k] . W^T.
-hipError_t launch_q4_gemm(const lgh_q4 *w, const int8_t *aq, const float *sa, float *y, size_t m,
-                          int mode, hipStream_t stream);
+// GEMM on an activation operand image: y[m][n] (+)= x[m][k] . W^T.
+// plan_q4_gemm_splits() is the number of K splits the launch wants for m
+// tokens; `part` holds part_floats floats of scratch, and the launch uses
+// fewer splits when splits * m * n would not fit.
+int plan_q4_gemm_splits(const lgh_q4 *w, size_t m);
+hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t m, int mode, float *part,
+                          size_t part_floats, hipStream_t stream);
 
 // Test hooks.
 hipError_t launch_q4_block_dots(const uint8_t *qs, const int8_t *a, size_t nblocks, int32_t *out,
                                 hipStream_t stream);
 hipError_t launch_q8_block_dots(const int8_t *qs, const int8_t *a, size_t nblocks, int32_t *out,
                                 hipStream_t stream);
-hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const int8_t *aq, size_t m, int32_t *out,
+// Exact block dots through the GEMM's operand images and matrix-core path:
+// mxa from launch_act_split_mx, out[m][n][bpr].
+hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const uint8_t *mxa, size_t m, int32_t *out,
                                      hipStream_t stream);
 
 }  // namespace lgh

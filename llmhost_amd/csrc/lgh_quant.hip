@@ -194,11 +194,134 @@ __global__ void q8_block_dots_kernel(const int8_t *__restrict__ qs, const int8_t
   out[b] = dot_q8_block(wp[0], wp[1], ap[0], ap[1]);
 }
 
+// ---- GEMM operand images ---------------------------------------------------
+// Weights: one thread per (tile t, pair p, block slot s, row r).  Element e of
+// a repacked nibble block sits in dword e/8, byte e%4, high nibble iff e%8 >= 4.
+__global__ void q4_mx_pack_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc, int n,
+                                  int bpr, int nt, int pp, uint8_t *mx) {
+  const size_t id = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= static_cast<size_t>(nt) * pp * 64) return;
+  const int r = static_cast<int>(id & 31), s = static_cast<int>((id >> 5) & 1);
+  const size_t rec = id >> 6;  // t * pp + p
+  const int t = static_cast<int>(rec / pp), p = static_cast<int>(rec % pp);
+  const int row = t * 32 + r, b = 2 * p + s;
+  uint32_t d[6] = {0, 0, 0, 0, 0, 0};
+  float scale = 0.0f;
+  if (row < n && b < bpr) {
+    const size_t blk = static_cast<size_t>(row) * bpr + b;
+    const uint4 w = reinterpret_cast<const uint4 *>(qs)[blk];
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 32; e++) {
+      const uint32_t byte = (wd[e >> 3] >> (8 * (e & 3))) & 0xFFu;
+      const uint32_t nib = (e & 4) ? (byte >> 4) : (byte & 0xFu);
+      const int v = static_cast<int>(nib ^ 8u) - 8;  // sign-extend 4 bits
+      const uint32_t code = e3m2_code(v);
+      const int bit = 6 * e;
+      d[bit >> 5] |= code << (bit & 31);
+      if ((bit & 31) > 26) d[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
+    }
+    scale = h2f(sc[blk]);
+  }
+  uint8_t *tile = mx + rec * kMxWRec + s * kMxTile;
+  *reinterpret_cast<uint4 *>(tile + r * 16) = make_uint4(d[0], d[1], d[2], d[3]);
+  *reinterpret_cast<uint2 *>(tile + 512 + r * 8) = make_uint2(d[4], d[5]);
+  reinterpret_cast<float *>(mx + rec * kMxWRec + 2 * kMxTile)[s * 32 + r] = scale;
+}
+
+// Store the h and l code dwords of one (token, block) group: dword 3*quad + r
+// of the block comes from lane r < 3 of each quad (pack24_group8).
+__device__ __forceinline__ void store_hl_group8(uint8_t *rec, int s, int tok, uint32_t vh, uint32_t vl) {
+  const uint32_t dh = pack24_group8(vh);
+  const uint32_t dl = pack24_group8(vl);
+  const int g = threadIdx.x & 7, r = g & 3;
+  if (r < 3) {
+    const uint32_t off = mx_dword_off(tok, 3 * (g >> 2) + r);
+    *reinterpret_cast<uint32_t *>(rec + (2 * s) * kMxTile + off) = dh;
+    *reinterpret_cast<uint32_t *>(rec + (2 * s + 1) * kMxTile + off) = dl;
+  }
+}
+
+// Activations: one 8-lane group per (token, block) over the padded ranges
+// [0, 32*mt) x [0, 2*pp), blocks fastest so x is read contiguously.
+__global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, int m, int bpr,
+                                                                int pp, int per_row,
+                                                                const float *row_scale, size_t groups,
+                                                                uint8_t *mxa) {
+  const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
+  if (gi >= groups) return;  // whole 8-lane groups exit together
+  const int g = threadIdx.x & 7;
+  const int t = static_cast<int>(gi / (2 * pp)), b = static_cast<int>(gi % (2 * pp));
+  const bool ok = t < m && b < bpr;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (ok) v = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
+  const bool pr = ok && per_row;
+  const float rs = pr ? row_scale[t] : 0.0f;
+  float scale;
+  int sum;
+  const int q = act_quant_group8(v, pr, rs, scale, sum);
+  uint32_t vh, vl;
+  codes24_hl(q, vh, vl);
+  uint8_t *rec = mxa + (static_cast<size_t>(t >> 5) * pp + (b >> 1)) * kMxARec;
+  store_hl_group8(rec, b & 1, t & 31, vh, vl);
+  if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = ok ? scale : 0.0f;
+}
+
+__global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__restrict__ aq, int m, int bpr,
+                                                                int pp, size_t groups, uint8_t *mxa) {
+  const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
+  if (gi >= groups) return;
+  const int g = threadIdx.x & 7;
+  const int t = static_cast<int>(gi / (2 * pp)), b = static_cast<int>(gi % (2 * pp));
+  int q = 0;
+  if (t < m && b < bpr) q = reinterpret_cast<const int *>(aq)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
+  uint32_t vh, vl;
+  codes24_hl(q, vh, vl);
+  uint8_t *rec = mxa + (static_cast<size_t>(t >> 5) * pp + (b >> 1)) * kMxARec;
+  store_hl_group8(rec, b & 1, t & 31, vh, vl);
+  if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = 0.0f;
+}
+
 inline unsigned blocks_for(size_t items, unsigned per) {
   return static_cast<unsigned>((items + per - 1) / per);
 }
 
 }  // namespace
+
+hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t st) {
+  const size_t threads = w->nt * w->pp * 64;
+  if (!threads) return hipSuccess;
+  hipLaunchKernelGGL(q4_mx_pack_kernel, dim3(blocks_for(threads, 256)), dim3(256), 0, st, w->qs, w->sc,
+                     static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(w->nt),
+                     static_cast<int>(w->pp), w->mx);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, uint8_t *mxa, float *row_scale,
+                               hipStream_t st) {
+  const size_t bpr = k / 32, pp = (bpr + 1) / 2, mt = (m + 31) / 32;
+  if (m == 0 || bpr == 0) return hipSuccess;
+  if (per_row) {
+    hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x,
+                       static_cast<int>(k), row_scale);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const size_t groups = mt * 32 * pp * 2;
+  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale, groups,
+                     mxa);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_split_mx(const int8_t *aq, size_t m, size_t k, uint8_t *mxa, hipStream_t st) {
+  const size_t bpr = k / 32, pp = (bpr + 1) / 2, mt = (m + 31) / 32;
+  if (m == 0 || bpr == 0) return hipSuccess;
+  const size_t groups = mt * 32 * pp * 2;
+  hipLaunchKernelGGL(act_split_mx_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, aq,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), groups, mxa);
+  return hipGetLastError();
+}
 
 hipError_t launch_q4_repack(const uint8_t *raw, size_t nblocks, uint8_t *qs, uint16_t *sc,
                             hipStream_t st) {

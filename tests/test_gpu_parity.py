@@ -9,7 +9,7 @@ and its VNNI kernel (the production CPU path) on identical seeded inputs.
 import numpy as np
 import pytest
 
-from llmhost_amd import q4, synth
+from llmhost_amd import formats, q4, synth
 from llmhost_amd.formats import BLOCK_Q4
 
 from .conftest import assert_close
@@ -101,6 +101,28 @@ def test_mfma_block_dots_bit_exact(gpu_ctx, oracle, n, k, m):
             for b in range(bpr):
                 ref[t, r, b] = oracle.dot_q4_q8(blocks[r * bpr + b], qs[t, b * 32:(b + 1) * 32])
     assert np.array_equal(got, ref)
+
+
+def test_mfma_block_dots_extremes(gpu_ctx, oracle):
+    """Largest block dots: nibbles -8 / 7 against activations -127 / 127 (|dot| = 32512),
+    plus every h/l split boundary of the activation codes (q = 16h + l)."""
+    n, k, m = 32, 64, 34
+    nib = np.where((np.arange(n) % 2 == 0)[:, None], -8, 7) * np.ones((1, k), dtype=np.int8)
+    nib[3, ::3] = 0
+    nib = nib.astype(np.int8)
+    blocks = formats.q4_from_nibbles(nib.reshape(-1, 32), np.full(n * k // 32, 0x3C00, dtype=np.uint16))
+    qs = np.empty((m, k), dtype=np.int8)
+    qs[0], qs[1] = -127, 127
+    qs[2:] = ((np.arange((m - 2) * k) % 255) - 127).reshape(m - 2, k).astype(np.int8)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = q4.q4_mfma_block_dots(w, qs, m)
+    ref = np.einsum("rbe,tbe->trb", nib.reshape(n, k // 32, 32).astype(np.int64),
+                    qs.reshape(m, k // 32, 32).astype(np.int64)).astype(np.int32)
+    assert np.abs(ref).max() == 32512
+    assert np.array_equal(got, ref)
+    for r in range(n):
+        for b in range(k // 32):
+            assert ref[5, r, b] == oracle.dot_q4_q8(blocks[r * (k // 32) + b], qs[5, b * 32:(b + 1) * 32])
 
 
 def test_upload_download_roundtrip(gpu_ctx):
@@ -201,7 +223,7 @@ def test_gemv_pair(gpu_ctx, oracle):
 # ---- GEMM -----------------------------------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(2, 48, 64), (4, 8192, 2048), (16, 512, 2048), (20, 48, 64),
                                    (40, 48, 64), (64, 1000, 2048), (100, 257, 320), (512, 256, 2048),
-                                   (130, 2048, 10752)])
+                                   (130, 2048, 10752), (33, 70, 96), (257, 130, 1056)])
 def test_gemm_matches_oracle(gpu_ctx, oracle, m, n, k):
     blocks = synth.q4_blocks(n + 7 * k, n, k)
     x = synth.activations(m + 3 * k, m, k)
