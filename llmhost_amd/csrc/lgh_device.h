@@ -184,15 +184,24 @@ __device__ __forceinline__ float recip_rn(float s) {
   return q;
 }
 
-// clamp(round_half_away_from_zero(v * inv), -127, 127) from inv2 = 2 * inv:
-// i = trunc(2y) exactly (RN(v * 2inv) = 2 RN(v * inv)), and for an integer
-// i = trunc(2y), round_half_away(y) = (i + (i < 0 ? -1 : 0) + 1) >> 1 with an
-// arithmetic shift (y >= 0: floor((floor(2y) + 1) / 2); y < 0: floor(i / 2)).
-// NaN converts to 0, like Rust's `NaN as i8`.
+// clamp(round_half_away_from_zero(v * inv), -127, 127) from a finite
+// inv2 = 2 * inv: i = trunc(2y) exactly (RN(v * 2inv) = 2 RN(v * inv)), and
+// for an integer i = trunc(2y), round_half_away(y) = (i + (i < 0 ? -1 : 0) + 1)
+// >> 1 with an arithmetic shift (y >= 0: floor((floor(2y) + 1) / 2); y < 0:
+// floor(i / 2)).  |v| <= amax keeps |v * inv2| below 256, so i never
+// saturates.  NaN converts to 0, like Rust's `NaN as i8`.
 __device__ __forceinline__ int quant_code(float v, float inv2) {
   const int i = static_cast<int>(v * inv2);  // v_cvt_i32_f32 truncates
   const int q = (i + (i >> 31) + 1) >> 1;
   return min(max(q, -127), 127);
+}
+
+// The reference's own arithmetic, `(v * inv).round().clamp(-127.0, 127.0) as
+// i8`, for blocks whose scale is below 2^-127 (2 * inv overflows, and inv
+// itself may be inf): clamp keeps NaN and a NaN cast is 0.
+__device__ __forceinline__ int quant_code_ref(float v, float inv) {
+  const float r = fminf(fmaxf(roundf(v * inv), -127.0f), 127.0f);
+  return (v * inv) != (v * inv) ? 0 : static_cast<int>(r);
 }
 
 // ActQ8 quantization of one 32-element block by a group of 8 lanes
@@ -211,11 +220,20 @@ __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float ro
   amax = fmaxf(amax, dpp<0x4E>(amax));
   amax = fmaxf(amax, dpp<0x141>(amax));
   scale = per_row ? row_scale : div127_rn(amax);
-  const float inv2 = scale == 0.0f ? 0.0f : 2.0f * recip_rn(scale);
-  const int q0 = quant_code(v.x, inv2);
-  const int q1 = quant_code(v.y, inv2);
-  const int q2 = quant_code(v.z, inv2);
-  const int q3 = quant_code(v.w, inv2);
+  const float inv = scale == 0.0f ? 0.0f : recip_rn(scale);
+  const float inv2 = 2.0f * inv;
+  int q0, q1, q2, q3;
+  if (inv2 <= 0x1.fffffep127f) {  // uniform per group; false only for scale < 2^-127
+    q0 = quant_code(v.x, inv2);
+    q1 = quant_code(v.y, inv2);
+    q2 = quant_code(v.z, inv2);
+    q3 = quant_code(v.w, inv2);
+  } else {
+    q0 = quant_code_ref(v.x, inv);
+    q1 = quant_code_ref(v.y, inv);
+    q2 = quant_code_ref(v.z, inv);
+    q3 = quant_code_ref(v.w, inv);
+  }
   int s = q0 + q1 + q2 + q3;
   s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xf, 0xf, false);
   s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xf, 0xf, false);

@@ -92,6 +92,13 @@ static float amax32(const float *src) {
 
 static float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+/* `x.round().clamp(lo, hi) as i8` in Rust: clamp keeps NaN, and a NaN cast
+ * to an integer type is 0 (saturating casts). */
+static int8_t rust_round_clamp_i8(float x, float lo, float hi) {
+  float r = clampf(roundf(x), lo, hi);
+  return r != r ? (int8_t)0 : (int8_t)r;
+}
+
 /* lib.rs:26-37 BlockQ8_0::quantize */
 void oq_q8_quantize(const float src[32], oq_block_q8 *dst) {
   float amax = amax32(src);
@@ -99,7 +106,7 @@ void oq_q8_quantize(const float src[32], oq_block_q8 *dst) {
   float scale_f = oq_f16_to_f32(scale);
   float inv = scale_f == 0.0f ? 0.0f : 1.0f / scale_f;
   dst->scale = scale;
-  for (int i = 0; i < OQ_BLOCK; i++) dst->qs[i] = (int8_t)clampf(roundf(src[i] * inv), -127.0f, 127.0f);
+  for (int i = 0; i < OQ_BLOCK; i++) dst->qs[i] = rust_round_clamp_i8(src[i] * inv, -127.0f, 127.0f);
 }
 
 /* lib.rs:40-45 BlockQ8_0::dequantize */
@@ -117,7 +124,7 @@ void oq_q4_quantize(const float src[32], oq_block_q4 *dst) {
   dst->scale = scale;
   memset(dst->qs, 0, sizeof dst->qs);
   for (int i = 0; i < OQ_BLOCK; i++) {
-    int8_t q = (int8_t)clampf(roundf(src[i] * inv), -8.0f, 7.0f);
+    int8_t q = rust_round_clamp_i8(src[i] * inv, -8.0f, 7.0f);
     uint8_t nib = (uint8_t)q & 0x0fu;
     if ((i & 1) == 0)
       dst->qs[i / 2] = nib;
@@ -172,7 +179,7 @@ static void act_quantize_row(const float *x, size_t k, int per_row, int8_t *qs,
     float inv = scale == 0.0f ? 0.0f : 1.0f / scale;
     int32_t sum = 0;
     for (int i = 0; i < OQ_BLOCK; i++) {
-      int8_t q = (int8_t)clampf(roundf(src[i] * inv), -127.0f, 127.0f);
+      int8_t q = rust_round_clamp_i8(src[i] * inv, -127.0f, 127.0f);
       qs[b * OQ_BLOCK + i] = q;
       sum += q;
     }
