@@ -246,9 +246,10 @@ def cpu_baseline(target_s: float = 12.0):
 
 def counters_mode(iters: int = 50) -> None:
     """Eager launches for hardware-counter runs (rocprofv3 --pmc): `iters`
-    launches of each headline GEMV over rotating copies, then a plain 64 MiB
-    device-to-device copy (torch) of known size to calibrate FETCH_SIZE /
-    WRITE_SIZE against.  Prints the byte counts each kernel should move."""
+    launches of each headline GEMV over rotating copies, 5 prefill GEMMs
+    (M=512, K=2048, N=10752), then a plain 64 MiB device-to-device copy
+    (torch) of known size to calibrate FETCH_SIZE / WRITE_SIZE against.
+    Prints the byte counts each kernel should move."""
     gb = GpuBench()
     torch, q4 = gb.torch, gb.q4
     from llmhost_amd import synth
@@ -265,6 +266,17 @@ def counters_mode(iters: int = 50) -> None:
             f"(weights {n * (k // 32) * 18})")
         for w in mats:
             w.free()
+    m, n, k = 512, 10752, 2048
+    _, mats = gb.copies(n, k, 401, 1)
+    x = torch.from_numpy(synth.activations(402, m, k)).cuda()
+    y = torch.zeros(m, n, device="cuda")
+    with torch.cuda.stream(gb.stream):
+        for _ in range(5):
+            q4.gemm_q4(mats[0], x, y, m)
+    torch.cuda.synchronize()
+    log(f"[counters] gemm M={m} K={k} N={n}: 5 launches, {2 * m * n * k} int8 ops each")
+    for w in mats:
+        w.free()
     src = torch.ones(16 << 20, device="cuda")
     dst = torch.empty_like(src)
     with torch.cuda.stream(gb.stream):
@@ -272,6 +284,23 @@ def counters_mode(iters: int = 50) -> None:
             dst.copy_(src)
     torch.cuda.synchronize()
     log(f"[counters] copy: {iters} launches of a 64 MiB read + 64 MiB write")
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_hbm_traffic.txt")
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch of the headline GEMV `name` (up / down) from the
+    committed PMC summary (FETCH_SIZE and WRITE_SIZE, copy-calibrated), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 3 and parts[0] == "traffic" and parts[1] == name:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -332,7 +361,7 @@ def main():
                    "global_batch": 1, "seq_len": 1, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": f"q4_gemv ({dom_name}: K={dom['k']}, N={dom['n']})",
                      "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
                      "bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3)},
         "cpu_baseline": cpu,
         "extra": extra,
@@ -340,7 +369,10 @@ def main():
     if "prefill_gemm_m512_k2048_n10752" in extra:
         g = extra["prefill_gemm_m512_k2048_n10752"]
         out["gemm_m512"] = {"tops": round(g["tops"], 2), "frac_int8_peak": round(g["frac_int8"], 4),
-                            "us": round(g["us"], 2)}
+                            "us": round(g["us"], 2),
+                            "roofline": {"bound": "mfma", "achieved": round(g["tops"], 2),
+                                         "peak": INT8_PEAK_TOPS, "unit": "TOPS (int8 dense)",
+                                         "frac": round(g["frac_int8"], 4)}}
     print(json.dumps(out), flush=True)
 
 

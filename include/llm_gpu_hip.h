@@ -156,9 +156,10 @@ int lgh_q4_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t 
 /* Integer Q8_0 x Q8 block dot (crates/llm-engine/src/weights.rs:206-209). */
 int lgh_q8_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks,
                       int32_t *out);
-/* Per-block integer dots of the GEMM's int8 MFMA path: out[m, n, k/32] =
- * sum over block kb of nibble(W[n]) * qs[m] (qs int8 [m, k]); checks the MFMA
- * operand layout bit-exactly against dot_q4_q8_scalar. */
+/* Per-block integer dots through the GEMM's matrix-core path (the matrix's
+ * fp6 operand image, the activations' h/l split, the scaled MFMA):
+ * out[m, n, k/32] = sum over block kb of nibble(W[n]) * qs[m] (qs int8
+ * [m, k]); bit-exact target dot_q4_q8_scalar (gemv_q4.rs:959-966). */
 int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size_t m,
                            int32_t *out);
 
