@@ -1,20 +1,20 @@
 // M = 1 kernels for gfx950: fused activation-quant + Q4 / Q8_0 GEMV.
 //
 // Q4 GEMV (replaces crates/llm-cpu/src/gemv_q4.rs:344-443, 499-667):
-//   * a workgroup of 16 waves owns a tile of rows; its waves form
-//     (16/KW row groups) x (KW K slices).  A wave owns R rows and one slice
-//     of 64*S blocks; lane l walks blocks l, l+64, ... of that slice;
+//   * each 16-lane DPP row of a wave owns one weight row, so a wave covers 4
+//     rows; a workgroup of W waves is (W/KW) row groups x KW K slices, and
+//     lane c of a row walks blocks slice*16*BPL + c + 16j (j < BPL);
 //   * issue order: (1) this thread's float4s of x, (2) every weight load of
-//     the lane -- R*S 128-bit nibble loads + R*S f16 scale loads, all
+//     the lane -- BPL 128-bit nibble loads + BPL f16 scale loads, all
 //     branch-free raw buffer loads (out of range -> 0) -- then (3) the ActQ8
-//     quantization of x into LDS, shared by the 16 waves, which waits only
+//     quantization of x into LDS, shared by the workgroup, which waits only
 //     for (1), so the HBM latency of (2) overlaps the prologue;
 //   * per block: 8 v_dot4_i32_i8 of the unpacked nibbles (x16) against the
 //     LDS codes, acc = fma(f32(16*idot), sw*sa, acc) -- the VNNI kernel's fold
 //     (gemv_q4.rs:659-661) in a different summation order;
-//   * a DPP wave reduction gives each row's slice sum; slice sums meet in LDS
-//     and are added in slice order (deterministic), then Assign or AddF64
-//     (gemv_q4.rs:486-497) after removing the x16 (exact).
+//   * 4 DPP adds give every lane of a DPP row its row's slice sum; slice sums
+//     meet in LDS and are added in slice order (deterministic), then Assign
+//     or AddF64 (gemv_q4.rs:486-497) after removing the x16 (exact).
 #include "lgh_device.h"
 #include "lgh_internal.h"
 
@@ -24,8 +24,6 @@ namespace {
 
 constexpr int kThreads = 256;  // Q8_0 GEMV workgroup
 constexpr int kWaves = kThreads / kWave;
-constexpr int kGemvWaves = 16;  // Q4 GEMV workgroup: 1024 threads
-constexpr int kGemvThreads = kGemvWaves * kWave;
 
 struct Q4GemvArgs {
   const uint8_t *qs0;
@@ -95,16 +93,18 @@ __device__ __forceinline__ void store_row(float *y, int row, float acc16, int mo
     y[row] = v;
 }
 
-// R rows per wave, S k-steps of 64 blocks per wave and slice, KW slices.
-template <int R, int S, int KW>
-__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(Q4GemvArgs a) {
-  constexpr int KB = 64 * S * KW;  // blocks covered by the workgroup (>= bpr)
-  constexpr int RG = kGemvWaves / KW;  // row groups
-  constexpr int XJ = (KB * 8 + kGemvThreads - 1) / kGemvThreads;
+// BPL blocks per lane and row, KW K slices, W waves; 4*(W/KW) rows per workgroup.
+template <int BPL, int KW, int W>
+__global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
+  constexpr int THREADS = W * kWave;
+  constexpr int KB = 16 * BPL * KW;  // blocks covered by the workgroup (>= bpr)
+  constexpr int RG = W / KW;
+  constexpr int XJ = (KB * 8 + THREADS - 1) / THREADS;
+  static_assert(W % KW == 0, "slices divide the waves");
   __shared__ __align__(16) int8_t s_qs[KB * 32];
   __shared__ float s_sa[KB];
-  __shared__ float s_red[kGemvWaves];
-  __shared__ float s_part[KW > 1 ? RG * R * KW : 1];
+  __shared__ float s_red[W];
+  __shared__ float s_part[KW > 1 ? RG * 4 * KW : 1];
   const int bpr = a.bpr;
   int wg = blockIdx.x;
   const uint8_t *qs = a.qs0;
@@ -120,81 +120,67 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(Q4GemvArgs a) {
   const int lane = tid & (kWave - 1);
   const int wave = uniform(tid / kWave);
   const int rg = wave / KW, ks = wave % KW;
-  const int row0 = (wg * RG + rg) * R;
-  const int rows = uniform(max(0, min(R, a.n - row0)));
-  const int kb_slice = ks * 64 * S;
+  const int row0 = (wg * RG + rg) * 4;  // first row of this wave
+  const int rows = uniform(max(0, min(4, a.n - row0)));
+  const int r = lane >> 4, c = lane & 15;
+  const int kb0 = ks * 16 * BPL + c;
 
   // (1) x: bpr*8 float4s, XJ per thread.
   const auto xr = make_rsrc(a.x, static_cast<uint32_t>(bpr) * 128u);
   float4 xv[XJ];
 #pragma unroll
-  for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * kGemvThreads) * 16u);
+  for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
 
-  // (2) every weight load of this lane.
+  // (2) every weight load of this lane (rows past n fall outside the resource).
   const size_t blk0 = static_cast<size_t>(row0) * bpr;
   const auto wr = make_rsrc(qs + blk0 * 16, static_cast<uint32_t>(rows * bpr) * 16u);
   const auto sr = make_rsrc(sc + blk0, static_cast<uint32_t>(rows * bpr) * 2u);
-  uint4 w[S][R];
-  uint16_t s[S][R];
+  uint4 w[BPL];
+  uint16_t s[BPL];
 #pragma unroll
-  for (int st = 0; st < S; st++) {
-    const int kb = kb_slice + st * kWave + lane;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
-      w[st][r] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 16u : kOOB);
-      s[st][r] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
-    }
+  for (int j = 0; j < BPL; j++) {
+    const int kb = kb0 + 16 * j;
+    const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
+    w[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 16u : kOOB);
+    s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
   }
 
   // (3) x -> LDS codes.
-  quantize_regs_to_lds<kGemvThreads, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
+  quantize_regs_to_lds<THREADS, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
 
   // (4) dots + fold.
-  float acc[R];
+  float acc = 0.0f;
 #pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = 0.0f;
-#pragma unroll
-  for (int st = 0; st < S; st++) {
-    const int kb = kb_slice + st * kWave + lane;
+  for (int j = 0; j < BPL; j++) {
+    const int kb = kb0 + 16 * j;
     if (kb < bpr) {
       const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kb * 32);
-      const v4i a0 = ap[0], a1 = ap[1];
-      const float sa = s_sa[kb];
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const int d = dot_q4_block16(w[st][r], a0, a1);
-        acc[r] = fmaf(static_cast<float>(d), h2f(s[st][r]) * sa, acc[r]);
-      }
+      const int d = dot_q4_block16(w[j], ap[0], ap[1]);
+      acc = fmaf(static_cast<float>(d), h2f(s[j]) * s_sa[kb], acc);
     }
   }
-  float t[R];
-#pragma unroll
-  for (int r = 0; r < R; r++) t[r] = wave_sum_dpp(acc[r]);
-
-  // (5) combine slices in slice order, then the epilogue.
+  // (5) 16-lane row sums (every lane of a DPP row ends with its row's sum).
+  acc += dpp<0xB1>(acc);   // quad_perm [1,0,3,2]
+  acc += dpp<0x4E>(acc);   // quad_perm [2,3,0,1]
+  acc += dpp<0x141>(acc);  // row_half_mirror
+  acc += dpp<0x140>(acc);  // row_mirror
   if constexpr (KW == 1) {
-#pragma unroll
-    for (int r = 0; r < R; r++)
-      if (lane == 0 && r < rows) store_row(y, row0 + r, t[r], a.mode);
+    if (c == 0 && r < rows) store_row(y, row0 + r, acc, a.mode);
   } else {
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < R; r++) s_part[(rg * R + r) * KW + ks] = t[r];
-    }
+    if (c == 0) s_part[(rg * 4 + r) * KW + ks] = acc;
     __syncthreads();
     if (ks == 0 && lane < rows) {
       float sum = 0.0f;
 #pragma unroll
-      for (int k = 0; k < KW; k++) sum += s_part[(rg * R + lane) * KW + k];
+      for (int k = 0; k < KW; k++) sum += s_part[(rg * 4 + lane) * KW + k];
       store_row(y, row0 + lane, sum, a.mode);
     }
   }
 }
 
-template <int R, int S, int KW>
-hipError_t launch_rsk(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
-  hipLaunchKernelGGL((q4_gemv_kernel<R, S, KW>), dim3(total_wgs), dim3(kGemvThreads), 0, st, a);
+template <int BPL, int KW, int W>
+hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
+  hipLaunchKernelGGL((q4_gemv_kernel<BPL, KW, W>), dim3(total_wgs), dim3(W * kWave), 0, st, a);
   return hipGetLastError();
 }
 
@@ -278,14 +264,21 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(Q8GemvArgs a) {
 // waves while every lane keeps its R weight loads in registers.
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat) {
   Q4GemvPlan p{};
-  p.S = 1;
-  p.KW = 1;
-  while (p.KW < kGemvWaves && static_cast<size_t>(64 * p.KW) < bpr) p.KW <<= 1;
-  p.ok = static_cast<size_t>(64 * p.KW) >= bpr;
-  int r = 4;
-  while (r > 1 && (n * nmat * p.KW) / static_cast<size_t>(r) < 4096) r >>= 1;
-  p.R = r;
-  const int rows_per_wg = (kGemvWaves / p.KW) * r;
+  if (bpr <= 64) {  // one slice: 16 lanes x BPL blocks cover the row
+    p.KW = 1;
+    p.BPL = static_cast<int>(bpr == 0 ? 1 : (bpr + 15) / 16);
+  } else {          // 2 blocks per lane, KW slices of 32 blocks (4 per lane for K > 16384)
+    p.BPL = bpr > 512 ? 4 : 2;
+    p.KW = 4;
+    while (p.KW < 16 && static_cast<size_t>(16 * p.BPL * p.KW) < bpr) p.KW <<= 1;
+  }
+  p.ok = static_cast<size_t>(16 * p.BPL * p.KW) >= bpr;
+  // Waves per workgroup: the largest of 16 / 8 / 4 (>= KW) that still gives
+  // >= 192 workgroups; every workgroup re-quantizes all of x, so fewer and
+  // larger workgroups win as long as most CUs stay busy.
+  p.W = 16;
+  while (p.W > 4 && p.W > p.KW && n * nmat / static_cast<size_t>(4 * p.W / p.KW) < 192) p.W >>= 1;
+  const int rows_per_wg = 4 * p.W / p.KW;
   p.wgs_per_mat = static_cast<int>((n + rows_per_wg - 1) / rows_per_wg);
   return p;
 }
@@ -295,7 +288,7 @@ hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *
   if (w0->n == 0) return hipSuccess;
   const int nmat = w1 ? 2 : 1;
   const Q4GemvPlan p = plan_q4_gemv(w0->n, w0->bpr, nmat);
-  if (!p.ok) return hipErrorInvalidValue;  // K > 32768: the API uses the GEMM
+  if (!p.ok) return hipErrorInvalidValue;  // K > 16384 * 2: the API uses the GEMM
   Q4GemvArgs a{};
   a.qs0 = w0->qs;
   a.sc0 = w0->sc;
@@ -310,24 +303,28 @@ hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *
   a.mode = mode;
   a.per_row = per_row;
   const int total = p.wgs_per_mat * nmat;
-#define LGH_RSK(RR, SS, KK) \
-  if (p.R == RR && p.S == SS && p.KW == KK) return launch_rsk<RR, SS, KK>(a, total, st)
-  LGH_RSK(4, 1, 1);
-  LGH_RSK(2, 1, 1);
-  LGH_RSK(1, 1, 1);
-  LGH_RSK(4, 1, 2);
-  LGH_RSK(2, 1, 2);
-  LGH_RSK(1, 1, 2);
-  LGH_RSK(4, 1, 4);
-  LGH_RSK(2, 1, 4);
-  LGH_RSK(1, 1, 4);
-  LGH_RSK(4, 1, 8);
-  LGH_RSK(2, 1, 8);
-  LGH_RSK(1, 1, 8);
-  LGH_RSK(4, 1, 16);
-  LGH_RSK(2, 1, 16);
-  LGH_RSK(1, 1, 16);
-#undef LGH_RSK
+#define LGH_G16(BB, KK, WW) \
+  if (p.BPL == BB && p.KW == KK && p.W == WW) return launch_gemv16<BB, KK, WW>(a, total, st)
+  LGH_G16(1, 1, 16);
+  LGH_G16(1, 1, 8);
+  LGH_G16(1, 1, 4);
+  LGH_G16(2, 1, 16);
+  LGH_G16(2, 1, 8);
+  LGH_G16(2, 1, 4);
+  LGH_G16(3, 1, 16);
+  LGH_G16(3, 1, 8);
+  LGH_G16(3, 1, 4);
+  LGH_G16(4, 1, 16);
+  LGH_G16(4, 1, 8);
+  LGH_G16(4, 1, 4);
+  LGH_G16(2, 4, 16);
+  LGH_G16(2, 4, 8);
+  LGH_G16(2, 4, 4);
+  LGH_G16(2, 8, 16);
+  LGH_G16(2, 8, 8);
+  LGH_G16(2, 16, 16);
+  LGH_G16(4, 16, 16);
+#undef LGH_G16
   return hipErrorInvalidValue;
 }
 

@@ -102,10 +102,11 @@ hipError_t launch_q8_quantize(const float *w, size_t nblocks, int8_t *qs, uint16
                               hipStream_t stream);
 
 // GEMV: y = W x for one or two matrices sharing x (pair).  w1 may be null.
-// plan.ok is false when K is longer than one workgroup covers (K > 32768):
-// the API then runs the batched act-quant + GEMM path with m = 1.
+// A workgroup of W waves covers 4*W/KW rows; each wave 4 rows x one K slice
+// of 16*BPL blocks.  plan.ok is false when K is longer than one workgroup
+// covers (K > 32768): the API then runs the act-quant + GEMM path with m = 1.
 struct Q4GemvPlan {
-  int R, S, KW, wgs_per_mat;
+  int BPL, KW, W, wgs_per_mat;
   bool ok;
 };
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat);
