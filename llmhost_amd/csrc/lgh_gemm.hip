@@ -20,9 +20,10 @@
 //
 // Workgroup = 4 waves in a WN x WM grid, each owning TN x TM 32x32 tiles.
 // K advances one block pair per stage.  A stage is the verbatim concatenation
-// of NS weight records and MS activation records (lgh_internal.h), copied by
-// 16-byte chunks through registers into one of two LDS buffers; the copy of
-// stage p+1 is in flight while stage p is computed, one barrier per stage.
+// of NS weight records and MS activation records (lgh_internal.h), copied
+// global -> LDS by buffer_load ... lds (DMA: no registers, no VALU) into one
+// of three LDS buffers; stages p+1 and p+2 are in flight while stage p is
+// computed, one barrier per stage.
 #include "lgh_device.h"
 #include "lgh_internal.h"
 
@@ -49,71 +50,101 @@ template <int WN, int WM, int TN, int TM>
 struct Cfg {
   static constexpr int NS = WN * TN;  // 32-row weight tiles per workgroup
   static constexpr int MS = WM * TM;  // 32-token tiles per workgroup
-  static constexpr int W_CH = NS * kWRec / 16;
+  static constexpr int W_CH = NS * kWRec / 16;  // 16-byte chunks per stage
   static constexpr int A_CH = MS * kARec / 16;
-  static constexpr int W_LD = (W_CH + kThreads - 1) / kThreads;
-  static constexpr int A_LD = (A_CH + kThreads - 1) / kThreads;
-  // Each region is padded to whole 256-chunk slots so every thread stores
-  // every slot without a branch (the padding receives zeros).
-  static constexpr int A_LDS = W_LD * kThreads * 16;  // activation records start here in a stage
-  static constexpr int STAGE = A_LDS + A_LD * kThreads * 16;
-  static constexpr int LDS = 2 * STAGE;
+  // A stage is copied by "wave loads" of 64 chunks (1 KB, one DMA
+  // instruction of a wave); every wave issues WPW of them per stage, the
+  // ones past the data load zeros into the padding.
+  static constexpr int WL_W = W_CH / 64;                       // weight wave loads
+  static constexpr int WL = WL_W + (A_CH + 63) / 64;           // all wave loads
+  static constexpr int WPW = (WL + kThreads / 64 - 1) / (kThreads / 64);
+  static constexpr int A_LDS = NS * kWRec;  // activation records start here in a stage
+  static constexpr int STAGE = WPW * (kThreads / 64) * 1024;
   static_assert(WN * WM * 64 == kThreads, "4 waves per workgroup");
+  static_assert(W_CH % 64 == 0, "weight records fill whole wave loads (NS % 4 == 0)");
   static_assert(kWRec % 16 == 0 && kARec % 16 == 0, "records are 16-byte chunks");
 };
 
-template <class C>
-struct Stage {
-  uint4 w[C::W_LD];
-  uint4 a[C::A_LD];
-};
-
-// Byte offsets (stage 0) of this thread's chunks in the two images; kOOB for
-// slots past the stage.  Tiles past nt / mt land past the image end and load
-// as zeros through the buffer range check.
+// Byte offsets (stage 0) of this lane's chunk in each of its wave's loads,
+// kOOB for padding loads.  Tiles past nt / mt land past the image end and
+// load as zeros through the buffer range check.
 template <class C>
 struct Slots {
-  uint32_t w[C::W_LD];
-  uint32_t a[C::A_LD];
+  uint32_t off[C::WPW];
 };
 
 template <class C>
-__device__ __forceinline__ void init_slots(const GemmArgs &g, int nt0, int mt0, Slots<C> &s) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void init_slots(const GemmArgs &g, int wave, int nt0, int mt0, Slots<C> &s) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < C::W_LD; i++) {
-    const int c = tid + i * kThreads;
-    const int t = c / (kWRec / 16), off = (c % (kWRec / 16)) * 16;
-    s.w[i] = c < C::W_CH ? static_cast<uint32_t>((nt0 + t) * g.pp) * kWRec + off : kOOB;
-  }
-#pragma unroll
-  for (int i = 0; i < C::A_LD; i++) {
-    const int c = tid + i * kThreads;
-    const int t = c / (kARec / 16), off = (c % (kARec / 16)) * 16;
-    s.a[i] = c < C::A_CH ? static_cast<uint32_t>((mt0 + t) * g.pp) * kARec + off : kOOB;
+  for (int i = 0; i < C::WPW; i++) {
+    const int j = wave + 4 * i;  // wave load index within the stage
+    if (j < C::WL_W) {
+      const int c = 64 * j + lane;
+      s.off[i] = static_cast<uint32_t>((nt0 + c / (kWRec / 16)) * g.pp) * kWRec + (c % (kWRec / 16)) * 16;
+    } else {
+      const int c = 64 * (j - C::WL_W) + lane;
+      s.off[i] = c < C::A_CH
+                     ? static_cast<uint32_t>((mt0 + c / (kARec / 16)) * g.pp) * kARec + (c % (kARec / 16)) * 16
+                     : kOOB;
+    }
   }
 }
 
-// Stage p >= pend (prefetches issued during the last stages) loads zeros.
-template <class C>
-__device__ __forceinline__ void load_stage(const GemmArgs &g, const Slots<C> &s, int p, int pend, Stage<C> &st) {
-  const auto rw = make_rsrc(g.wmx, g.w_bytes);
-  const auto ra = make_rsrc(g.amx, g.a_bytes);
-  const bool live = p < pend;
-  const uint32_t dw = static_cast<uint32_t>(p) * kWRec, da = static_cast<uint32_t>(p) * kARec;
-#pragma unroll
-  for (int i = 0; i < C::W_LD; i++) st.w[i] = buf_load16(rw, (s.w[i] == kOOB || !live) ? kOOB : s.w[i] + dw);
-#pragma unroll
-  for (int i = 0; i < C::A_LD; i++) st.a[i] = buf_load16(ra, (s.a[i] == kOOB || !live) ? kOOB : s.a[i] + da);
+typedef __attribute__((address_space(3))) void lds_void;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (SGPR quad) for an image of `bytes` bytes: out-of-range
+// offsets read as 0.
+__device__ __forceinline__ i32x4 sgpr_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = uniform(static_cast<int>(a & 0xffffffffu));
+  r[1] = uniform(static_cast<int>((a >> 32) & 0xffffu));  // stride 0
+  r[2] = uniform(static_cast<int>(bytes));
+  r[3] = kBufDword3;
+  return r;
 }
 
+// One wave load: lane l's 16 bytes from rsrc + voff + soff land at LDS byte
+// address lds + 16 l (buffer_load_dwordx4 ... lds, address base in M0).
+// Issued as inline asm so that the compiler does not see an LDS write it
+// would have to fence conservatively; the pipeline waits for it explicitly
+// (vmcnt).  voff must stay live (loop-invariant): a VMEM instruction may read
+// its address VGPR after issue.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const char *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void *)p));
+}
+
+// DMA stage p of this workgroup's operand records into `buf` (global ->
+// LDS, no registers): wave load j lands at buf + 1 KB * j.  Record p sits at
+// a uniform offset p * record size from record 0, passed as soffset.  The
+// hardware range check is only guaranteed on the VGPR offset, so every
+// address is kept inside the image by construction: record-0 offsets of
+// tiles past the image and of padding slots are >= 2^31 (out of range ->
+// zeros), and a stage p >= pend (prefetched past the end of the range, never
+// computed) re-reads stage pend - 1.
 template <class C>
-__device__ __forceinline__ void store_stage(char *buf, const Stage<C> &st) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void dma_stage(const GemmArgs &g, const Slots<C> &s, int wave, int p, int pend,
+                                          const char *buf) {
+  const i32x4 rw = sgpr_rsrc(g.wmx, g.w_bytes);
+  const i32x4 ra = sgpr_rsrc(g.amx, g.a_bytes);
+  const uint32_t base = lds_addr(buf);
+  const int q = uniform(min(p, pend - 1));
+  const uint32_t sw = static_cast<uint32_t>(q * kWRec), sa = static_cast<uint32_t>(q * kARec);
 #pragma unroll
-  for (int i = 0; i < C::W_LD; i++) *reinterpret_cast<uint4 *>(buf + (tid + i * kThreads) * 16) = st.w[i];
-#pragma unroll
-  for (int i = 0; i < C::A_LD; i++) *reinterpret_cast<uint4 *>(buf + C::A_LDS + (tid + i * kThreads) * 16) = st.a[i];
+  for (int i = 0; i < C::WPW; i++) {
+    const int j = wave + 4 * i;  // wave-uniform: the selects below are scalar
+    const bool wt = j < C::WL_W;
+    dma16(wt ? rw : ra, s.off[i], wt ? sw : sa, base + 1024u * static_cast<uint32_t>(j));
+  }
 }
 
 // One stage of the inner loop for a wave's TN x TM tiles: per tile, the
@@ -155,26 +186,39 @@ __device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, f
     }
 }
 
-// Stage p: `spent` held stage p (already in LDS) and is refilled with stage
-// p+2; `next` holds stage p+1 and goes to the other LDS buffer after the
-// compute.  The sched_barrier keeps that store -- and its wait for the
-// global loads -- behind the MFMAs and folds.
-// LDS buffer (p - p0) & 1 holds stage p.
+// Wait until at most N of this wave's vector-memory operations are in
+// flight and its LDS operations are done, then meet the workgroup.  The
+// "memory" clobber keeps every LDS access on its side of the barrier.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// Stage p, held in `cur`; `nxt2` (read during stage p-1) receives stage p+2.
+// The wait leaves only stage p+1's DMAs of this wave in flight; after the
+// barrier every wave's DMAs of stage p are complete and every wave is done
+// reading `nxt2`.
 template <class C, int TN, int TM>
-__device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int p, int p0, int pend,
-                                              char *lds, int wn, int wm, float (&acc)[TN][TM][16], Stage<C> &spent,
-                                              Stage<C> &next) {
-  load_stage<C>(g, slots, p + 2, pend, spent);
-  compute_stage<C, TN, TM>(lds + ((p - p0) & 1) * C::STAGE, wn, wm, acc);
+__device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int wave, int p, int pend,
+                                              const char *cur, char *nxt2, int wn, int wm,
+                                              float (&acc)[TN][TM][16]) {
+  wait_vm_barrier<C::WPW>();
+  dma_stage<C>(g, slots, wave, p + 2, pend, nxt2);
+  compute_stage<C, TN, TM>(cur, wn, wm, acc);
+  // Keep each stage's MFMAs and folds inside the stage: interleaving them
+  // with the next stage's only lengthens register lifetimes.
   __builtin_amdgcn_sched_barrier(0);
-  store_stage<C>(lds + ((p - p0 + 1) & 1) * C::STAGE, next);
-  __syncthreads();
 }
 
 template <int WN, int WM, int TN, int TM>
 __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
   using C = Cfg<WN, WM, TN, TM>;
-  extern __shared__ __align__(16) char lds[];
+  // Three stage buffers as distinct objects, so the compiler can tell the
+  // buffer being read from the ones the DMA is filling.
+  __shared__ __align__(1024) char lds0[C::STAGE];
+  __shared__ __align__(1024) char lds1[C::STAGE];
+  __shared__ __align__(1024) char lds2[C::STAGE];
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int wn = wave % WN, wm = wave / WN;
@@ -190,25 +234,25 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
       for (int v = 0; v < 16; v++) acc[tn][tm][v] = 0.0f;
 
   Slots<C> slots;
-  init_slots<C>(g, nt0, mt0, slots);
-  // Two register stages in flight: while stage p is computed from LDS, stage
-  // p+1 waits in registers for its LDS store and stage p+2 is being fetched.
+  init_slots<C>(g, wave, nt0, mt0, slots);
   // Split z of the K range: block pairs [p0, pend).
   const int z = blockIdx.z;
   const int p0 = static_cast<int>(static_cast<long>(g.pp) * z / g.splits);
   const int pend = static_cast<int>(static_cast<long>(g.pp) * (z + 1) / g.splits);
-  Stage<C> s0, s1;
-  load_stage<C>(g, slots, p0, pend, s0);
-  load_stage<C>(g, slots, p0 + 1, pend, s1);
-  store_stage<C>(lds, s0);
-  __syncthreads();
-
+  dma_stage<C>(g, slots, wave, p0, pend, lds0);
+  dma_stage<C>(g, slots, wave, p0 + 1, pend, lds1);
+  // Unrolled by three so every stage's buffer roles are static.
   int p = p0;
-  for (; p + 1 < pend; p += 2) {
-    pipeline_step<C, TN, TM>(g, slots, p, p0, pend, lds, wn, wm, acc, s0, s1);
-    pipeline_step<C, TN, TM>(g, slots, p + 1, p0, pend, lds, wn, wm, acc, s1, s0);
+  for (; p + 2 < pend; p += 3) {
+    pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, acc);
+    pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, acc);
+    pipeline_step<C, TN, TM>(g, slots, wave, p + 2, pend, lds2, lds1, wn, wm, acc);
   }
-  if (p < pend) pipeline_step<C, TN, TM>(g, slots, p, p0, pend, lds, wn, wm, acc, s0, s1);
+  if (p < pend) pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, acc);
+  if (p + 1 < pend) pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, acc);
+  // Drain the prefetches of stages past pend before the workgroup can exit
+  // (their LDS must not be written after it is released).
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 
   // With split K the partial sums go to part[z] (assign); a second kernel
   // adds the splits in order and applies the caller's mode.
@@ -301,7 +345,7 @@ hipError_t launch_cfg(GemmArgs g, int splits, float *part, hipStream_t st) {
   g.splits = splits;
   g.part = part;
   const dim3 grid((g.nt + C::NS - 1) / C::NS, (g.mt + C::MS - 1) / C::MS, splits);
-  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), C::LDS, st, g);
+  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), 0, st, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, st, part,
