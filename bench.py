@@ -191,11 +191,11 @@ def gemm_case(gb: GpuBench, m, n, k, iters, seed):
             "frac_int8": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "gbs": byts / (ms * 1e-3) / 1e9}
 
 
-def q8_case(gb: GpuBench, iters):
+def q8_case(gb: GpuBench, iters, n=1536, k=1536):
+    """Q8_0 GEMV (q8_apply) over rotating copies (> 2x MALL)."""
     torch, q4 = gb.torch, gb.q4
     from llmhost_amd import synth
 
-    n = k = 1536
     b8 = synth.q8_blocks(71, n, k)
     count = math.ceil(2 * MALL_BYTES / (n * (k // 32) * 34))
     mats = [q4.Q8Matrix.from_blocks(n, k, b8, gb.ctx) for _ in range(count)]
@@ -204,7 +204,24 @@ def q8_case(gb: GpuBench, iters):
     ms = gb.timed(lambda i: q4.q8_apply(mats[i % count], x, 1, y), iters, 10)
     for w in mats:
         w.free()
-    return {"us": ms * 1e3, "gbs": q8_bytes(n, k) / (ms * 1e-3) / 1e9}
+    return {"n": n, "k": k, "us": ms * 1e3, "gbs": q8_bytes(n, k) / (ms * 1e-3) / 1e9,
+            "frac_hbm": q8_bytes(n, k) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def q4_head_case(gb: GpuBench, iters, n=65536, k=1536):
+    """Q4 GEMV at the tied-head shape (the alternative to the Q8_0 head)."""
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    _, mats = gb.copies(n, k, 81, 2 * MALL_BYTES)
+    x = torch.from_numpy(synth.normal_f32(82, k)).cuda()
+    y = torch.zeros(n, device="cuda")
+    C = len(mats)
+    ms = gb.timed(lambda i: q4.gemv_q4(mats[i % C], x, y), iters, 5)
+    for w in mats:
+        w.free()
+    return {"n": n, "k": k, "us": ms * 1e3, "gbs": q4_bytes(n, k) / (ms * 1e-3) / 1e9,
+            "frac_hbm": q4_bytes(n, k) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
 def cpu_baseline(target_s: float = 12.0):
@@ -339,6 +356,9 @@ def main():
             extra[f"prefill_gemm_m{m}_k{k}_n{n}"] = gemm_case(gb, m, n, k, 10, 400 + m + k)
         log("[bench] q8 gemv")
         extra["q8_gemv_k1536_n1536"] = q8_case(gb, 200)
+        log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
+        extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
+        extra["q4_head_k1536_n65536"] = q4_head_case(gb, 20)
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")

@@ -355,11 +355,23 @@ hipError_t launch_cfg(GemmArgs g, int splits, float *part, hipStream_t st) {
 
 }  // namespace
 
+// Workgroup tile by batch size: 128 rows x 32 / 64 tokens for small batches
+// and up to M = 768 (more, smaller workgroups keep two or more resident per
+// CU), 128 x 128 above (operand reuse wins once every CU holds several).
+// Long K (> 8192) keeps 128 x 128: split K then supplies the workgroups.
+enum class GemmCfg { k128x32, k128x64, k128x128 };
+static GemmCfg gemm_cfg(size_t m, size_t pp) {
+  if (m > 32 && m <= 64) return GemmCfg::k128x64;
+  return (m <= 32 || (m <= 768 && pp <= 128)) ? GemmCfg::k128x32 : GemmCfg::k128x128;
+}
+
 int plan_q4_gemm_splits(const lgh_q4 *w, size_t m) {
   const size_t mt = (m + 31) / 32;
-  if (m <= 32) return splits_for<4, 1, 1, 1>(w->nt, mt, w->pp);
-  if (m <= 64) return splits_for<4, 1, 1, 2>(w->nt, mt, w->pp);
-  return splits_for<2, 2, 2, 2>(w->nt, mt, w->pp);
+  switch (gemm_cfg(m, w->pp)) {
+    case GemmCfg::k128x32: return splits_for<4, 1, 1, 1>(w->nt, mt, w->pp);
+    case GemmCfg::k128x64: return splits_for<4, 1, 1, 2>(w->nt, mt, w->pp);
+    default: return splits_for<2, 2, 2, 2>(w->nt, mt, w->pp);
+  }
 }
 
 hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t m, int mode, float *part,
@@ -382,9 +394,11 @@ hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t 
              1,
              static_cast<uint32_t>(w->nt * w->pp * kMxWRec),
              static_cast<uint32_t>(mt * w->pp * kMxARec)};
-  if (m <= 32) return launch_cfg<4, 1, 1, 1>(g, splits, part, st);  // 128 rows x 32 tokens
-  if (m <= 64) return launch_cfg<4, 1, 1, 2>(g, splits, part, st);  // 128 x 64
-  return launch_cfg<2, 2, 2, 2>(g, splits, part, st);               // 128 x 128
+  switch (gemm_cfg(m, w->pp)) {
+    case GemmCfg::k128x32: return launch_cfg<4, 1, 1, 1>(g, splits, part, st);
+    case GemmCfg::k128x64: return launch_cfg<4, 1, 1, 2>(g, splits, part, st);
+    default: return launch_cfg<2, 2, 2, 2>(g, splits, part, st);
+  }
 }
 
 hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const uint8_t *mxa, size_t m, int32_t *out,
