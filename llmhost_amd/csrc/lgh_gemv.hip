@@ -184,6 +184,161 @@ hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---- batched Q4 GEMV, 2 <= M <= 16 ----------------------------------------
+// Small ragged batches (crates/llm-cpu/src/gemv_q4.rs:686-722 with m <= 16)
+// are weight-stream bound like the GEMV, so they read the 18-byte nibble
+// blocks once and dot each against T token code rows held in LDS: per block
+// one nibble unpack, then 8 v_dot4_i32_i8 and one fold per token.  Same row
+// mapping, slices and DPP row sums as q4_gemv_kernel.  The codes come either
+// from quantizing x[T][k] in the prologue (QUANT, small T * k) or, already
+// quantized by act_quant_kernel, from int8 qs[m][k] + f32 scales[m][bpr].
+struct Q4BatchArgs {
+  const uint8_t *qs;
+  const uint16_t *sc;
+  const float *x;      // QUANT: f32 [m][k]
+  const int8_t *aq;    // !QUANT: int8 [m][k]
+  const float *as;     // !QUANT: f32 [m][bpr]
+  float *y;            // [m][n]
+  int n, bpr, m, mode, per_row;
+};
+
+template <int T, int BPL, int KW, int W, bool QUANT>
+__global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a) {
+  constexpr int THREADS = W * kWave;
+  constexpr int KB = 16 * BPL * KW;
+  constexpr int RG = W / KW;
+  static_assert(W % KW == 0, "slices divide the waves");
+  __shared__ __align__(16) int8_t s_qs[T][KB * 32];
+  __shared__ float s_sa[T][KB];
+  __shared__ float s_red[W];
+  __shared__ float s_part[KW > 1 ? RG * 4 * KW * T : 1];
+  const int bpr = a.bpr;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = uniform(tid / kWave);
+  const int rg = wave / KW, ks = wave % KW;
+  const int row0 = (blockIdx.x * RG + rg) * 4;
+  const int rows = uniform(max(0, min(4, a.n - row0)));
+  const int r = lane >> 4, c = lane & 15;
+  const int kb0 = ks * 16 * BPL + c;
+
+  // (1) activations: x rows (QUANT) or codes + scales; tokens >= m read as 0.
+  constexpr int XJ = QUANT ? (KB * 8 + THREADS - 1) / THREADS : 1;
+  float4 xv[T][XJ];
+  if constexpr (QUANT) {
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const auto xr = make_rsrc(a.x + static_cast<size_t>(t) * bpr * 32, t < a.m ? static_cast<uint32_t>(bpr) * 128u : 0u);
+#pragma unroll
+      for (int j = 0; j < XJ; j++) xv[t][j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+    }
+  } else {
+    const auto qr = make_rsrc(a.aq, static_cast<uint32_t>(a.m * bpr) * 32u);
+    const auto sr = make_rsrc(a.as, static_cast<uint32_t>(a.m * bpr) * 4u);
+    for (int i = tid; i < T * bpr * 2; i += THREADS) {  // 16-byte chunks of [T][bpr][32]
+      const int t = i / (bpr * 2), rem = i % (bpr * 2);
+      const uint4 v = buf_load16(qr, t < a.m ? static_cast<uint32_t>((t * bpr) * 32 + rem * 16) : kOOB);
+      *reinterpret_cast<uint4 *>(&s_qs[t][rem * 16]) = v;
+    }
+    for (int i = tid; i < T * bpr; i += THREADS) {
+      const int t = i / bpr, b = i % bpr;
+      s_sa[t][b] = buf_load_f32(sr, t < a.m ? static_cast<uint32_t>(t * bpr + b) * 4u : kOOB);
+    }
+  }
+
+  // (2) every weight load of this lane.
+  const size_t blk0 = static_cast<size_t>(row0) * bpr;
+  const auto wr = make_rsrc(a.qs + blk0 * 16, static_cast<uint32_t>(rows * bpr) * 16u);
+  const auto swr = make_rsrc(a.sc + blk0, static_cast<uint32_t>(rows * bpr) * 2u);
+  uint4 w[BPL];
+  uint16_t s[BPL];
+#pragma unroll
+  for (int j = 0; j < BPL; j++) {
+    const int kb = kb0 + 16 * j;
+    const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
+    w[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 16u : kOOB);
+    s[j] = buf_load_u16(swr, kb < bpr ? blk * 2u : kOOB);
+  }
+
+  // (3) codes into LDS (QUANT), one barrier.
+  if constexpr (QUANT) {
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const float rs = row_scale_of<THREADS, XJ>(xv[t], a.per_row, s_red);
+      quant_regs<THREADS, XJ>(xv[t], bpr, a.per_row != 0, rs, s_qs[t], s_sa[t]);
+    }
+  } else {
+    __syncthreads();
+  }
+
+  // (4) per block: one unpack, then T dots and folds.
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < BPL; j++) {
+    const int kb = kb0 + 16 * j;
+    if (kb < bpr) {
+      const int u[8] = {nib_lo16(w[j].x), nib_hi16(w[j].x), nib_lo16(w[j].y), nib_hi16(w[j].y),
+                        nib_lo16(w[j].z), nib_hi16(w[j].z), nib_lo16(w[j].w), nib_hi16(w[j].w)};
+      const float sw = h2f(s[j]);
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const v4i *ap = reinterpret_cast<const v4i *>(&s_qs[t][kb * 32]);
+        const v4i a0 = ap[0], a1 = ap[1];
+        int d = sdot4(u[0], a0.x, 0);
+        d = sdot4(u[1], a0.y, d);
+        d = sdot4(u[2], a0.z, d);
+        d = sdot4(u[3], a0.w, d);
+        d = sdot4(u[4], a1.x, d);
+        d = sdot4(u[5], a1.y, d);
+        d = sdot4(u[6], a1.z, d);
+        d = sdot4(u[7], a1.w, d);
+        acc[t] = fmaf(static_cast<float>(d), sw * s_sa[t][kb], acc[t]);
+      }
+    }
+  }
+  // (5) row sums, slices in order, epilogue per token.
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    acc[t] += dpp<0xB1>(acc[t]);
+    acc[t] += dpp<0x4E>(acc[t]);
+    acc[t] += dpp<0x141>(acc[t]);
+    acc[t] += dpp<0x140>(acc[t]);
+  }
+  if constexpr (KW == 1) {
+    if (c == 0 && r < rows) {
+#pragma unroll
+      for (int t = 0; t < T; t++)
+        if (t < a.m) store_row(a.y + static_cast<size_t>(t) * a.n, row0 + r, acc[t], a.mode);
+    }
+  } else {
+    if (c == 0) {
+#pragma unroll
+      for (int t = 0; t < T; t++) s_part[((rg * 4 + r) * T + t) * KW + ks] = acc[t];
+    }
+    __syncthreads();
+    if (ks == 0 && lane < rows * T) {
+      const int rr = lane / T, t = lane % T;
+      if (t < a.m) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KW; k++) sum += s_part[((rg * 4 + rr) * T + t) * KW + k];
+        store_row(a.y + static_cast<size_t>(t) * a.n, row0 + rr, sum, a.mode);
+      }
+    }
+  }
+}
+
+template <int T, int BPL, int KW, bool QUANT>
+hipError_t launch_batch(const Q4BatchArgs &a, hipStream_t st) {
+  constexpr int W = 8;
+  const int rows_per_wg = 4 * W / KW;
+  const unsigned wgs = static_cast<unsigned>((a.n + rows_per_wg - 1) / rows_per_wg);
+  hipLaunchKernelGGL((q4_gemv_batch_kernel<T, BPL, KW, W, QUANT>), dim3(wgs), dim3(W * kWave), 0, st, a);
+  return hipGetLastError();
+}
+
 // ---- Q8_0 GEMV (crates/llm-engine/src/weights.rs:194-227) ---------------
 struct Q8GemvArgs {
   const int8_t *qs;
@@ -325,6 +480,56 @@ hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *
   LGH_G16(2, 16, 16);
   LGH_G16(4, 16, 16);
 #undef LGH_G16
+  return hipErrorInvalidValue;
+}
+
+Q4BatchPlan plan_q4_batch(size_t m, size_t bpr) {
+  Q4BatchPlan p{};
+  if (m < 2 || m > 16 || bpr == 0) return p;
+  p.T = m <= 4 ? 4 : (m <= 8 ? 8 : 16);
+  if (bpr <= 64) {
+    p.KW = 1;
+    p.BPL = static_cast<int>((bpr + 15) / 16);
+  } else if (bpr <= 128) {
+    p.KW = 2;
+    p.BPL = 4;
+  } else if (bpr <= 256) {
+    p.KW = 4;
+    p.BPL = 4;
+  } else {
+    return p;
+  }
+  // LDS holds T rows of codes: T * 16 * BPL * KW blocks <= 1024 (32 KB).
+  p.ok = p.T * 16 * p.BPL * p.KW <= 1024;
+  p.quant = p.T == 4;
+  return p;
+}
+
+hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *aq, const float *as, float *y,
+                                size_t m, int mode, int per_row, hipStream_t st) {
+  const Q4BatchPlan p = plan_q4_batch(m, w->bpr);
+  if (!p.ok) return hipErrorInvalidValue;
+  if (w->n == 0) return hipSuccess;
+  Q4BatchArgs a{w->qs, w->sc, x, aq, as, y, static_cast<int>(w->n), static_cast<int>(w->bpr),
+                static_cast<int>(m), mode, per_row};
+#define LGH_B(TT, BB, KK, QQ) \
+  if (p.T == TT && p.BPL == BB && p.KW == KK && p.quant == QQ) return launch_batch<TT, BB, KK, QQ>(a, st)
+  LGH_B(4, 1, 1, true);
+  LGH_B(4, 2, 1, true);
+  LGH_B(4, 3, 1, true);
+  LGH_B(4, 4, 1, true);
+  LGH_B(4, 4, 2, true);
+  LGH_B(4, 4, 4, true);
+  LGH_B(8, 1, 1, false);
+  LGH_B(8, 2, 1, false);
+  LGH_B(8, 3, 1, false);
+  LGH_B(8, 4, 1, false);
+  LGH_B(8, 4, 2, false);
+  LGH_B(16, 1, 1, false);
+  LGH_B(16, 2, 1, false);
+  LGH_B(16, 3, 1, false);
+  LGH_B(16, 4, 1, false);
+#undef LGH_B
   return hipErrorInvalidValue;
 }
 

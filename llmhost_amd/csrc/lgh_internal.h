@@ -112,6 +112,17 @@ struct Q4GemvPlan {
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);
+// Batched GEMV for 2 <= m <= 16 rows of x (ragged decode batches): T = 4 / 8
+// / 16 token slots; quant: the kernel quantizes x itself (T = 4), else it
+// reads int8 codes aq[m][k] + scales as[m][k/32] from act_quant.  ok is false
+// when the shape does not fit (the API then runs the MFMA GEMM).
+struct Q4BatchPlan {
+  int T, BPL, KW;
+  bool quant, ok;
+};
+Q4BatchPlan plan_q4_batch(size_t m, size_t bpr);
+hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *aq, const float *as, float *y,
+                                size_t m, int mode, int per_row, hipStream_t stream);
 // Q8_0 GEMV for k <= kQ8GemvMaxK.
 constexpr size_t kQ8GemvMaxK = 12288;
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens,

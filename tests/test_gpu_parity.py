@@ -235,6 +235,30 @@ def test_gemm_matches_oracle(gpu_ctx, oracle, m, n, k):
     assert_close(got, oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_VNNI, threads=8), what="vs vnni")
 
 
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("m,n,k", [(2, 37, 32), (3, 131, 96), (4, 260, 544), (5, 77, 2048), (8, 130, 3072),
+                                   (9, 67, 1024), (16, 301, 2048), (4, 129, 4096), (3, 45, 8192),
+                                   (8, 64, 4096), (16, 33, 1536)])
+def test_small_batch_gemv_path(gpu_ctx, oracle, per_row, m, n, k):
+    """2 <= m <= 16 runs the batched GEMV (token slots 4/8/16, 1/2/4 K slices): Assign and AddF64."""
+    blocks = synth.q4_blocks(m + n + k, n, k)
+    x = synth.activations(m * 7 + k, m, k)
+    y0 = synth.activations(n + 5, m, n)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        got = np.zeros((m, n), dtype=np.float32)
+        q4.gemm_q4(w, x, got, m)
+        added = y0.copy()
+        q4.gemm_q4_add(w, x, added, m)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    assert_close(got, oracle.gemm_q4(mat, x, m, per_row=per_row, threads=8), what="batch assign")
+    assert_close(added, oracle.gemm_q4(mat, x, m, out=y0.copy(), add=True, per_row=per_row, threads=8),
+                 what="batch add")
+
+
 def test_gemm_matches_per_token_gemv_reference_inputs(gpu_ctx, oracle):
     """gemm_matches_per_token_gemv (gemv_q4.rs:1167-1195) and the AMX test (amx.rs:526-557)."""
     for n, k, m in [(48, 64, 20), (48, 64, 40)]:
