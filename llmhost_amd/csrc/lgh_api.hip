@@ -408,23 +408,25 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
   if (m == 1 && lgh::plan_q4_gemv(w->n, w->bpr, 1).ok) return lgh_q4_gemv_dev(ctx, w, x_dev, y_dev, mode);
-  const lgh::Q4BatchPlan bp = lgh::plan_q4_batch(m, w->bpr);
-  if (bp.ok) {  // small batches: weight-stream bound, nibble planes + dot4
+  // Small batches are weight-stream bound: nibble planes, no operand image.
+  if (lgh::plan_q4_batch(m, w->bpr).ok) {  // m <= 4: x quantized inside the kernel, dot4
     if (int r = set_device(ctx)) return r;
-    if (bp.quant) {
-      LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w, x_dev, nullptr, nullptr, y_dev, m, mode, ctx->act_mode, ctx->stream));
-      return LGH_OK;
-    }
+    LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w, x_dev, y_dev, m, mode, ctx->act_mode, ctx->stream));
+    return LGH_OK;
+  }
+  if (lgh::plan_q4_mma(w->n, m, w->bpr).ok) {  // m <= 64: activation image, then int8 MFMA per block
+    if (int r = set_device(ctx)) return r;
+    const size_t mt = (m + 15) / 16, pq = (w->bpr + 3) / 4;
     Carve cv;
-    const size_t o_qs = cv.take(m * w->k), o_sa = cv.take(m * w->bpr * sizeof(float));
+    const size_t o_ci = cv.take(mt * pq * 2 * 1024), o_si = cv.take(mt * pq * 256);
     const size_t o_rs = cv.take(m * sizeof(float));
     if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
     char *ws = static_cast<char *>(ctx->ws);
-    auto *qs = reinterpret_cast<int8_t *>(ws + o_qs);
-    auto *sa = reinterpret_cast<float *>(ws + o_sa);
-    LGH_HIP(ctx, lgh::launch_act_quant(x_dev, m, w->k, ctx->act_mode, qs, sa, nullptr,
-                                       reinterpret_cast<float *>(ws + o_rs), ctx->stream));
-    LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w, nullptr, qs, sa, y_dev, m, mode, ctx->act_mode, ctx->stream));
+    auto *ci = reinterpret_cast<uint8_t *>(ws + o_ci);
+    auto *si = reinterpret_cast<float *>(ws + o_si);
+    LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev, m, w->k, ctx->act_mode, ci, si,
+                                           reinterpret_cast<float *>(ws + o_rs), ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w, ci, si, y_dev, m, mode, ctx->stream));
     return LGH_OK;
   }
   if (!w->mx) return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w->n, w->k);

@@ -184,29 +184,27 @@ hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
   return hipGetLastError();
 }
 
-// ---- batched Q4 GEMV, 2 <= M <= 16 ----------------------------------------
-// Small ragged batches (crates/llm-cpu/src/gemv_q4.rs:686-722 with m <= 16)
-// are weight-stream bound like the GEMV, so they read the 18-byte nibble
-// blocks once and dot each against T token code rows held in LDS: per block
-// one nibble unpack, then 8 v_dot4_i32_i8 and one fold per token.  Same row
-// mapping, slices and DPP row sums as q4_gemv_kernel.  The codes come either
-// from quantizing x[T][k] in the prologue (QUANT, small T * k) or, already
-// quantized by act_quant_kernel, from int8 qs[m][k] + f32 scales[m][bpr].
+// ---- batched Q4 GEMV, 2 <= M <= 4 -----------------------------------------
+// Tiny ragged batches (crates/llm-cpu/src/gemv_q4.rs:686-722 with m <= 4) are
+// weight-stream bound like the GEMV and need no second launch: the workgroup
+// quantizes the T = 4 token rows of x in its prologue (cheap for so few
+// tokens), then reads each 18-byte nibble block once and dots it against the
+// T code rows in LDS: one nibble unpack, then 8 v_dot4_i32_i8 and one fold per
+// token.  Row mapping, slices and DPP row sums as in q4_gemv_kernel.
 struct Q4BatchArgs {
   const uint8_t *qs;
   const uint16_t *sc;
-  const float *x;      // QUANT: f32 [m][k]
-  const int8_t *aq;    // !QUANT: int8 [m][k]
-  const float *as;     // !QUANT: f32 [m][bpr]
-  float *y;            // [m][n]
+  const float *x;  // f32 [m][k]
+  float *y;        // [m][n]
   int n, bpr, m, mode, per_row;
 };
 
-template <int T, int BPL, int KW, int W, bool QUANT>
+template <int T, int BPL, int KW, int W>
 __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;
   constexpr int RG = W / KW;
+  constexpr int XJ = (KB * 8 + THREADS - 1) / THREADS;
   static_assert(W % KW == 0, "slices divide the waves");
   __shared__ __align__(16) int8_t s_qs[T][KB * 32];
   __shared__ float s_sa[T][KB];
@@ -222,31 +220,17 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
   const int r = lane >> 4, c = lane & 15;
   const int kb0 = ks * 16 * BPL + c;
 
-  // (1) activations: x rows (QUANT) or codes + scales; tokens >= m read as 0.
-  constexpr int XJ = QUANT ? (KB * 8 + THREADS - 1) / THREADS : 1;
+  // (1) the x rows (tokens >= m read as 0), issued before the weights so
+  // that waiting for them leaves the weight loads in flight.
   float4 xv[T][XJ];
-  if constexpr (QUANT) {
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-      const auto xr = make_rsrc(a.x + static_cast<size_t>(t) * bpr * 32, t < a.m ? static_cast<uint32_t>(bpr) * 128u : 0u);
+  for (int t = 0; t < T; t++) {
+    const auto xr = make_rsrc(a.x + static_cast<size_t>(t) * bpr * 32, t < a.m ? static_cast<uint32_t>(bpr) * 128u : 0u);
 #pragma unroll
-      for (int j = 0; j < XJ; j++) xv[t][j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
-    }
-  } else {
-    const auto qr = make_rsrc(a.aq, static_cast<uint32_t>(a.m * bpr) * 32u);
-    const auto sr = make_rsrc(a.as, static_cast<uint32_t>(a.m * bpr) * 4u);
-    for (int i = tid; i < T * bpr * 2; i += THREADS) {  // 16-byte chunks of [T][bpr][32]
-      const int t = i / (bpr * 2), rem = i % (bpr * 2);
-      const uint4 v = buf_load16(qr, t < a.m ? static_cast<uint32_t>((t * bpr) * 32 + rem * 16) : kOOB);
-      *reinterpret_cast<uint4 *>(&s_qs[t][rem * 16]) = v;
-    }
-    for (int i = tid; i < T * bpr; i += THREADS) {
-      const int t = i / bpr, b = i % bpr;
-      s_sa[t][b] = buf_load_f32(sr, t < a.m ? static_cast<uint32_t>(t * bpr + b) * 4u : kOOB);
-    }
+    for (int j = 0; j < XJ; j++) xv[t][j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
   }
 
-  // (2) every weight load of this lane.
+  // (2) every weight load of this lane (rows past n read as 0).
   const size_t blk0 = static_cast<size_t>(row0) * bpr;
   const auto wr = make_rsrc(a.qs + blk0 * 16, static_cast<uint32_t>(rows * bpr) * 16u);
   const auto swr = make_rsrc(a.sc + blk0, static_cast<uint32_t>(rows * bpr) * 2u);
@@ -260,15 +244,11 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
     s[j] = buf_load_u16(swr, kb < bpr ? blk * 2u : kOOB);
   }
 
-  // (3) codes into LDS (QUANT), one barrier.
-  if constexpr (QUANT) {
+  // (3) codes into LDS.
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-      const float rs = row_scale_of<THREADS, XJ>(xv[t], a.per_row, s_red);
-      quant_regs<THREADS, XJ>(xv[t], bpr, a.per_row != 0, rs, s_qs[t], s_sa[t]);
-    }
-  } else {
-    __syncthreads();
+  for (int t = 0; t < T; t++) {
+    const float rs = row_scale_of<THREADS, XJ>(xv[t], a.per_row, s_red);
+    quant_regs<THREADS, XJ>(xv[t], bpr, a.per_row != 0, rs, s_qs[t], s_sa[t]);
   }
 
   // (4) per block: one unpack, then T dots and folds.
@@ -330,12 +310,206 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
   }
 }
 
-template <int T, int BPL, int KW, bool QUANT>
+template <int BPL, int KW>
 hipError_t launch_batch(const Q4BatchArgs &a, hipStream_t st) {
   constexpr int W = 8;
   const int rows_per_wg = 4 * W / KW;
   const unsigned wgs = static_cast<unsigned>((a.n + rows_per_wg - 1) / rows_per_wg);
-  hipLaunchKernelGGL((q4_gemv_batch_kernel<T, BPL, KW, W, QUANT>), dim3(wgs), dim3(W * kWave), 0, st, a);
+  hipLaunchKernelGGL((q4_gemv_batch_kernel<4, BPL, KW, W>), dim3(wgs), dim3(W * kWave), 0, st, a);
+  return hipGetLastError();
+}
+
+// ---- batched Q4 GEMV on the matrix cores, 2 <= M <= 64 --------------------
+// The same weight stream, with the block dots of 16 weight rows x 16 tokens
+// on one v_mfma_i32_16x16x32_i8 per block (K = 32 = one block, so every
+// MFMA result is one exact block dot; cf. tdpbssd per K-block,
+// crates/llm-cpu/src/amx.rs:329-380) and the reference's per-block fold
+// acc = fma(f32(dot), sw * sa, acc) (gemv_q4.rs:930-936) on the 4 results a
+// lane holds.  Operands, in the MFMA's register layouts:
+//   A (16 rows x 32): lane l = row l%16, elements 8g..8g+7 (g = l/16) = dword
+//     g of the block's 16-byte nibble plane, unpacked x16 (the GEMV's unpack);
+//   B (32 x 16 tokens): lane l = token l%16, codes 8g..8g+7 of the block --
+//     8 bytes of the activation image act_quant_mma writes in this layout;
+//   D: lane l = token l%16, rows 4g..4g+3.
+// Weights arrive as 16-byte blocks (coalesced 64-byte runs per row) and are
+// transposed to dwords through a per-wave LDS tile (row stride padded to
+// avoid bank conflicts); no workgroup barrier until the K-slice reduction.
+// Workgroup = 4 waves = RG row groups of 16 rows x KW K-slices.
+struct Q4MmaArgs {
+  const uint8_t *qs;   // nibble plane [n][bpr][16]
+  const uint16_t *sc;  // f16 scales [n][bpr]
+  const uint8_t *ci;   // activation codes image [mt][2 pq][64][16]
+  const float *si;     // activation scales image [mt][pq][16][4]
+  float *y;            // [m][n]
+  int n, bpr, m, mode, mt, pq;
+};
+
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+// Registers of one K chunk (CB blocks) of a wave.
+template <int TT, int CB>
+struct MmaChunk {
+  static constexpr int WL = CB / 4;  // 16-byte weight loads per lane
+  static constexpr int SL = CB / 4;  // scale loads per lane
+  uint4 wv[WL];
+  uint16_t sv[SL];
+  uint4 bq[TT][CB / 2];  // B operands of block pairs
+  float4 sa[TT][CB / 4];  // activation scales of block quads (token lane % 16)
+};
+
+// Issue every load of chunk ch: weights (piece p = 64 i + lane is row p / CB,
+// block p % CB), weight scales (row lane / 4, blocks SL (lane % 4) + e), then
+// each token tile's B operands and scales from the activation image (one
+// contiguous 1 KB / 256 B run per instruction).
+template <int TT, int CB>
+__device__ __forceinline__ void mma_load(const Q4MmaArgs &a, __amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t sr,
+                                         __amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t ar, int ch,
+                                         MmaChunk<TT, CB> &c) {
+  using C = MmaChunk<TT, CB>;
+  const int lane = threadIdx.x & 63, lr = lane & 15;
+  const int bpr = a.bpr, kb0 = ch * CB;
+#pragma unroll
+  for (int i = 0; i < C::WL; i++) {
+    const int p = 64 * i + lane, r = p / CB, kb = kb0 + p % CB;
+    c.wv[i] = buf_load16<kAuxNT>(wr, kb < bpr ? static_cast<uint32_t>(r * bpr + kb) * 16u : kOOB);
+  }
+#pragma unroll
+  for (int e = 0; e < C::SL; e++) {
+    const int r = lane >> 2, kb = kb0 + C::SL * (lane & 3) + e;
+    c.sv[e] = buf_load_u16(sr, kb < bpr ? static_cast<uint32_t>(r * bpr + kb) * 2u : kOOB);
+  }
+#pragma unroll
+  for (int tt = 0; tt < TT; tt++) {
+    const bool tile = tt < a.mt;
+#pragma unroll
+    for (int j = 0; j < CB / 2; j++) {
+      const int pr = kb0 / 2 + j;  // block pair
+      c.bq[tt][j] = buf_load16(cr, tile && pr < 2 * a.pq ? static_cast<uint32_t>((tt * 2 * a.pq + pr) * 64 + lane) * 16u
+                                                          : kOOB);
+    }
+#pragma unroll
+    for (int j = 0; j < CB / 4; j++) {
+      const int qd = kb0 / 4 + j;  // block quad
+      c.sa[tt][j] = buf_load_f4(ar, tile && qd < a.pq ? static_cast<uint32_t>((tt * a.pq + qd) * 16 + lr) * 16u : kOOB);
+    }
+  }
+}
+
+// Transpose the chunk's weights and scales through this wave's LDS tile
+// (the same wave writes and reads it: LDS keeps a wave's accesses in order),
+// then one MFMA and 4 folds per block and token tile.  Blocks past the row
+// hold zero weights, scales and codes and add exactly 0 (no branches).
+template <int TT, int CB>
+__device__ __forceinline__ void mma_compute(const MmaChunk<TT, CB> &c, uint32_t *tw, float *tsw,
+                                            float (&acc)[TT][4]) {
+  using C = MmaChunk<TT, CB>;
+  constexpr int RS = CB * 4 + 4;  // row stride in dwords, padded against bank conflicts
+  const int lane = threadIdx.x & 63, lr = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < C::WL; i++) {
+    const int p = 64 * i + lane;
+    *reinterpret_cast<uint4 *>(&tw[(p / CB) * RS + (p % CB) * 4]) = c.wv[i];
+  }
+#pragma unroll
+  for (int e = 0; e < C::SL; e++) tsw[(C::SL * (lane & 3) + e) * 16 + (lane >> 2)] = h2f(c.sv[e]);
+#pragma unroll
+  for (int b = 0; b < CB; b++) {
+    const uint32_t dw = tw[lr * RS + b * 4 + g];
+    const long wa = static_cast<long>(static_cast<uint32_t>(nib_lo16(dw))) |
+                    (static_cast<long>(static_cast<uint32_t>(nib_hi16(dw))) << 32);
+    const float4 sw = *reinterpret_cast<const float4 *>(&tsw[b * 16 + 4 * g]);
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+      const uint4 bp = c.bq[tt][b / 2];
+      const long wb = (b & 1) ? (static_cast<long>(bp.z) | (static_cast<long>(bp.w) << 32))
+                              : (static_cast<long>(bp.x) | (static_cast<long>(bp.y) << 32));
+      const v4i32 zero = {0, 0, 0, 0};
+      const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, wb, zero, 0, 0, 0);
+      const float4 s4 = c.sa[tt][b / 4];
+      const float s = (b & 3) == 0 ? s4.x : (b & 3) == 1 ? s4.y : (b & 3) == 2 ? s4.z : s4.w;
+      acc[tt][0] = fmaf(static_cast<float>(d[0]), sw.x * s, acc[tt][0]);
+      acc[tt][1] = fmaf(static_cast<float>(d[1]), sw.y * s, acc[tt][1]);
+      acc[tt][2] = fmaf(static_cast<float>(d[2]), sw.z * s, acc[tt][2]);
+      acc[tt][3] = fmaf(static_cast<float>(d[3]), sw.w * s, acc[tt][3]);
+    }
+  }
+}
+
+// W = RG x KW waves: RG row groups of 16 rows, KW K slices.  The planner
+// gives each wave one chunk when the row allows it, so all of a wave's loads
+// are in flight at once (the GEMV's single round trip); longer rows loop.
+template <int TT, int KW, int CB, int RG>
+__global__ __launch_bounds__(RG * KW * 64) void q4_mma_kernel(Q4MmaArgs a) {
+  constexpr int W = RG * KW;
+  constexpr int RS = CB * 4 + 4;
+  static_assert(CB % 4 == 0 && CB <= 16, "chunk");
+  __shared__ __align__(16) uint32_t s_w[W][16 * RS];
+  __shared__ __align__(16) float s_sw[W][CB * 16];
+  __shared__ float s_part[KW > 1 ? W * TT * 4 * 64 : 1];
+  const int bpr = a.bpr;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int rg = wave / KW, ks = wave % KW;
+  const int row0 = (blockIdx.x * RG + rg) * 16;
+  const int rows = uniform(max(0, min(16, a.n - row0)));
+  const int lr = lane & 15, g = lane >> 4;  // A: row lr; B / D: token lr; K group g
+  const int nch = (bpr + CB - 1) / CB;
+  const int ch_lo = nch * ks / KW, ch_hi = nch * (ks + 1) / KW;
+
+  const size_t blk0 = static_cast<size_t>(row0) * bpr;
+  const auto wr = make_rsrc(a.qs + blk0 * 16, static_cast<uint32_t>(rows * bpr) * 16u);
+  const auto sr = make_rsrc(a.sc + blk0, static_cast<uint32_t>(rows * bpr) * 2u);
+  const auto cr = make_rsrc(a.ci, static_cast<uint32_t>(a.mt * 2 * a.pq) * 1024u);
+  const auto ar = make_rsrc(a.si, static_cast<uint32_t>(a.mt * a.pq) * 256u);
+
+  float acc[TT][4];
+#pragma unroll
+  for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) acc[tt][v] = 0.0f;
+
+  for (int ch = ch_lo; ch < ch_hi; ch++) {
+    MmaChunk<TT, CB> c;
+    mma_load<TT, CB>(a, wr, sr, cr, ar, ch, c);
+    mma_compute<TT, CB>(c, s_w[wave], s_sw[wave], acc);
+  }
+
+  // K slices meet in LDS and are added in slice order; D layout: token
+  // tt*16 + lr, rows 4g + v.
+  if constexpr (KW > 1) {
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) s_part[((wave * TT + tt) * 4 + v) * 64 + lane] = acc[tt][v];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KW; k++) sum += s_part[(((rg * KW + k) * TT + tt) * 4 + v) * 64 + lane];
+        acc[tt][v] = sum;
+      }
+  }
+#pragma unroll
+  for (int tt = 0; tt < TT; tt++) {
+    const int t = tt * 16 + lr;
+    if (t >= a.m) continue;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int r = 4 * g + v;
+      if (r < rows) store_row(a.y + static_cast<size_t>(t) * a.n, row0 + r, acc[tt][v], a.mode);
+    }
+  }
+}
+
+template <int TT, int KW, int CB, int RG>
+hipError_t launch_mma(const Q4MmaArgs &a, hipStream_t st) {
+  const int rows_per_wg = 16 * RG;
+  const unsigned wgs = static_cast<unsigned>((a.n + rows_per_wg - 1) / rows_per_wg);
+  hipLaunchKernelGGL((q4_mma_kernel<TT, KW, CB, RG>), dim3(wgs), dim3(RG * KW * 64), 0, st, a);
   return hipGetLastError();
 }
 
@@ -483,53 +657,84 @@ hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *
   return hipErrorInvalidValue;
 }
 
+// m <= 4 tokens in T = 4 slots; K: one slice of BPL <= 4 blocks per lane up
+// to 64 blocks, then 2 or 4 slices of 64 (the prologue quantizes 4 rows of
+// up to 8192 elements).  Other shapes run the matrix-core batch kernel.
 Q4BatchPlan plan_q4_batch(size_t m, size_t bpr) {
   Q4BatchPlan p{};
-  if (m < 2 || m > 16 || bpr == 0) return p;
-  p.T = m <= 4 ? 4 : (m <= 8 ? 8 : 16);
+  if (m < 2 || m > 4 || bpr == 0) return p;
   if (bpr <= 64) {
     p.KW = 1;
     p.BPL = static_cast<int>((bpr + 15) / 16);
-  } else if (bpr <= 128) {
-    p.KW = 2;
-    p.BPL = 4;
   } else if (bpr <= 256) {
-    p.KW = 4;
+    p.KW = bpr <= 128 ? 2 : 4;
     p.BPL = 4;
   } else {
     return p;
   }
-  // LDS holds T rows of codes: T * 16 * BPL * KW blocks <= 1024 (32 KB).
-  p.ok = p.T * 16 * p.BPL * p.KW <= 1024;
-  p.quant = p.T == 4;
+  p.ok = true;
   return p;
 }
 
-hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *aq, const float *as, float *y,
-                                size_t m, int mode, int per_row, hipStream_t st) {
+hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, float *y, size_t m, int mode, int per_row,
+                                hipStream_t st) {
   const Q4BatchPlan p = plan_q4_batch(m, w->bpr);
   if (!p.ok) return hipErrorInvalidValue;
   if (w->n == 0) return hipSuccess;
-  Q4BatchArgs a{w->qs, w->sc, x, aq, as, y, static_cast<int>(w->n), static_cast<int>(w->bpr),
-                static_cast<int>(m), mode, per_row};
-#define LGH_B(TT, BB, KK, QQ) \
-  if (p.T == TT && p.BPL == BB && p.KW == KK && p.quant == QQ) return launch_batch<TT, BB, KK, QQ>(a, st)
-  LGH_B(4, 1, 1, true);
-  LGH_B(4, 2, 1, true);
-  LGH_B(4, 3, 1, true);
-  LGH_B(4, 4, 1, true);
-  LGH_B(4, 4, 2, true);
-  LGH_B(4, 4, 4, true);
-  LGH_B(8, 1, 1, false);
-  LGH_B(8, 2, 1, false);
-  LGH_B(8, 3, 1, false);
-  LGH_B(8, 4, 1, false);
-  LGH_B(8, 4, 2, false);
-  LGH_B(16, 1, 1, false);
-  LGH_B(16, 2, 1, false);
-  LGH_B(16, 3, 1, false);
-  LGH_B(16, 4, 1, false);
-#undef LGH_B
+  Q4BatchArgs a{w->qs, w->sc, x, y, static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(m), mode,
+                per_row};
+  if (p.KW == 1) {
+    switch (p.BPL) {
+      case 1: return launch_batch<1, 1>(a, st);
+      case 2: return launch_batch<2, 1>(a, st);
+      case 3: return launch_batch<3, 1>(a, st);
+      default: return launch_batch<4, 1>(a, st);
+    }
+  }
+  return p.KW == 2 ? launch_batch<4, 2>(a, st) : launch_batch<4, 4>(a, st);
+}
+
+// Token tiles TT = ceil(m / 16) (<= 4); 8-block chunks; KW (a power of
+// two <= 8) K slices per 16 rows: one chunk per wave for one or two token
+// tiles, two for four (measured at N=8192, K=2048: more, smaller waves are
+// faster while a chunk's registers stay small, then occupancy wins); RG row
+// groups make the workgroup at least 4 waves.
+Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr) {
+  Q4MmaPlan p{};
+  if (m < 2 || m > 64 || bpr == 0 || n == 0) return p;
+  p.TT = static_cast<int>((m + 15) / 16);
+  if (p.TT == 3) p.TT = 4;
+  p.CB = 8;
+  const size_t nch = (bpr + p.CB - 1) / p.CB;
+  const size_t per_wave = p.TT == 4 ? 2 : 1;
+  p.KW = 1;
+  while (p.KW < 8 && static_cast<size_t>(p.KW) * per_wave < nch) p.KW *= 2;
+  p.RG = p.KW >= 4 ? 1 : 4 / p.KW;
+  p.ok = true;
+  return p;
+}
+
+hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
+                              int mode, hipStream_t st) {
+  const Q4MmaPlan p = plan_q4_mma(w->n, m, w->bpr);
+  if (!p.ok) return hipErrorInvalidValue;
+  Q4MmaArgs a{w->qs, w->sc, codes, scales, y, static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(m),
+              mode, static_cast<int>((m + 15) / 16), static_cast<int>((w->bpr + 3) / 4)};
+#define LGH_M(TT_, KW_, CB_, RG_) \
+  if (p.TT == TT_ && p.KW == KW_ && p.CB == CB_ && p.RG == RG_) return launch_mma<TT_, KW_, CB_, RG_>(a, st)
+  LGH_M(1, 1, 8, 4);
+  LGH_M(1, 2, 8, 2);
+  LGH_M(1, 4, 8, 1);
+  LGH_M(1, 8, 8, 1);
+  LGH_M(2, 1, 8, 4);
+  LGH_M(2, 2, 8, 2);
+  LGH_M(2, 4, 8, 1);
+  LGH_M(2, 8, 8, 1);
+  LGH_M(4, 1, 8, 4);
+  LGH_M(4, 2, 8, 2);
+  LGH_M(4, 4, 8, 1);
+  LGH_M(4, 8, 8, 1);
+#undef LGH_M
   return hipErrorInvalidValue;
 }
 

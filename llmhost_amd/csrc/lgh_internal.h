@@ -112,17 +112,33 @@ struct Q4GemvPlan {
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);
-// Batched GEMV for 2 <= m <= 16 rows of x (ragged decode batches): T = 4 / 8
-// / 16 token slots; quant: the kernel quantizes x itself (T = 4), else it
-// reads int8 codes aq[m][k] + scales as[m][k/32] from act_quant.  ok is false
-// when the shape does not fit (the API then runs the MFMA GEMM).
+// Batched GEMV for 2 <= m <= 4 rows of x, quantized inside the kernel
+// (one launch).  ok is false when the shape does not fit.
 struct Q4BatchPlan {
-  int T, BPL, KW;
-  bool quant, ok;
+  int BPL, KW;
+  bool ok;
 };
 Q4BatchPlan plan_q4_batch(size_t m, size_t bpr);
-hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *aq, const float *as, float *y,
-                                size_t m, int mode, int per_row, hipStream_t stream);
+hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, float *y, size_t m, int mode, int per_row,
+                                hipStream_t stream);
+// Batched GEMV on the matrix cores for 2 <= m <= 64 (TT 16-token tiles, KW
+// K slices, CB-block chunks, RG 16-row groups per workgroup) on an
+// activation image written by act_quant_mma, with mt = ceil(m/16) token
+// tiles and pq = ceil(k/128) block quads:
+//   codes  [mt][2*pq pairs][64 lanes][16 B]: lane (t, g) = token t (0..15),
+//          K group g (0..3) holds codes 8g..8g+7 of the pair's two blocks
+//          (the B operand of v_mfma_i32_16x16x32_i8, 8 bytes per block);
+//   scales [mt][pq][16 tokens][4 blocks] f32.
+// Padding tokens and blocks hold 0.
+struct Q4MmaPlan {
+  int TT, KW, CB, RG;
+  bool ok;
+};
+Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr);
+hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row, uint8_t *codes, float *scales,
+                                float *row_scale, hipStream_t stream);
+hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
+                              int mode, hipStream_t stream);
 // Q8_0 GEMV for k <= kQ8GemvMaxK.
 constexpr size_t kQ8GemvMaxK = 12288;
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens,

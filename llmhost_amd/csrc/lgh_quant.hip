@@ -282,6 +282,32 @@ __global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__
   if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = 0.0f;
 }
 
+// Activations for the matrix-core batch GEMV, in its MFMA register layouts
+// (lgh_internal.h): one 8-lane group per (token, block) over the padded
+// ranges [0, 16*mt) x [0, 4*pq); padding gets code 0 and scale 0.
+__global__ __launch_bounds__(kThreads) void act_quant_mma_kernel(const float *__restrict__ x, int m, int bpr,
+                                                                 int pq, int per_row, const float *row_scale,
+                                                                 size_t groups, uint8_t *codes, float *scales) {
+  const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
+  if (gi >= groups) return;  // whole 8-lane groups exit together
+  const int g8 = threadIdx.x & 7;
+  const int t = static_cast<int>(gi / (4 * pq)), b = static_cast<int>(gi % (4 * pq));
+  const bool ok = t < m && b < bpr;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (ok) v = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g8];
+  const bool pr = ok && per_row;
+  const float rs = pr ? row_scale[t] : 0.0f;
+  float scale;
+  int sum;
+  const int q = act_quant_group8(v, pr, rs, scale, sum);
+  // Codes 4 g8 .. 4 g8 + 3 of block b: lane (t % 16) + 16 (g8 / 2) of the
+  // block pair b / 2, bytes 8 (b % 2) + 4 (g8 % 2).
+  const size_t pair = static_cast<size_t>(t >> 4) * (2 * pq) + (b >> 1);
+  const int lane = (t & 15) + 16 * (g8 >> 1);
+  *reinterpret_cast<int *>(codes + (pair * 64 + lane) * 16 + (b & 1) * 8 + (g8 & 1) * 4) = q;
+  if (g8 == 0) scales[((static_cast<size_t>(t >> 4) * pq + (b >> 2)) * 16 + (t & 15)) * 4 + (b & 3)] = ok ? scale : 0.0f;
+}
+
 inline unsigned blocks_for(size_t items, unsigned per) {
   return static_cast<unsigned>((items + per - 1) / per);
 }
@@ -311,6 +337,23 @@ hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, 
   hipLaunchKernelGGL(act_quant_mx_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x,
                      static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale, groups,
                      mxa);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row, uint8_t *codes, float *scales,
+                                float *row_scale, hipStream_t st) {
+  const size_t bpr = k / 32, pq = (bpr + 3) / 4, mt = (m + 15) / 16;
+  if (m == 0 || bpr == 0) return hipSuccess;
+  if (per_row) {
+    hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x,
+                       static_cast<int>(k), row_scale);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const size_t groups = mt * 16 * pq * 4;
+  hipLaunchKernelGGL(act_quant_mma_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pq), per_row, row_scale, groups,
+                     codes, scales);
   return hipGetLastError();
 }
 
