@@ -150,8 +150,12 @@ __device__ __forceinline__ void dma_stage(const GemmArgs &g, const Slots<C> &s, 
 // One stage of the inner loop for a wave's TN x TM tiles: per tile, the
 // outer product of the two blocks' scales, the two blocks' exact dots, and
 // 32 FMAs folding them into the accumulators (block order as in the reference).
+// r16 / r8 = row * 16 / row * 8 for the second block's reads, opaque so the
+// compiler does not pair them with the first block's into one ds_read2 whose
+// result would then be split into the two operands by v_mov.
 template <class C, int TN, int TM>
-__device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, float (&acc)[TN][TM][16]) {
+__device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, int r16, int r8,
+                                              float (&acc)[TN][TM][16]) {
   const int lane = threadIdx.x & 63, row = lane & 31, half = lane >> 5;
   const v32f zero32 = {};
   // Scale inputs of the outer products: lane L holds block L/32, row or token
@@ -163,14 +167,14 @@ __device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, f
     const char *rec = buf + (wn * TN + tn) * kWRec;
     xs[tn] = reinterpret_cast<const float *>(rec + 2 * kTile)[lane];
     A[0][tn] = mx_row(rec, row);
-    A[1][tn] = mx_row(rec + kTile, row);
+    A[1][tn] = mx_row_at(rec + kTile, r16, r8);
   }
 #pragma unroll
   for (int tm = 0; tm < TM; tm++) {
     const char *rec = buf + C::A_LDS + (wm * TM + tm) * kARec;
     ys[tm] = reinterpret_cast<const float *>(rec + 4 * kTile)[lane];
     B[0][tm] = mx_row(rec + half * kTile, row);
-    B[1][tm] = mx_row(rec + (2 + half) * kTile, row);
+    B[1][tm] = mx_row_at(rec + (2 + half) * kTile, r16, r8);
   }
 #pragma unroll
   for (int tn = 0; tn < TN; tn++)
@@ -179,11 +183,20 @@ __device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, f
       const v32f P = __builtin_amdgcn_mfma_f32_32x32x1f32(xs[tn], ys[tm], zero32, 0, 0, 0);
       const v16f c0 = mx_block_dot(A[0][tn], B[0][tm]);
       const v16f c1 = mx_block_dot(A[1][tn], B[1][tm]);
+      // Both blocks' dots are issued before either is folded (the second
+      // block's MFMA overlaps the first block's folds); per element the
+      // blocks are added in order.
+      float t0[16];
 #pragma unroll
-      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c0[v], P[v], acc[tn][tm][v]);
+      for (int v = 0; v < 16; v++) t0[v] = fmaf(c0[v], P[v], acc[tn][tm][v]);
 #pragma unroll
-      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c1[v], P[16 + v], acc[tn][tm][v]);
+      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c1[v], P[16 + v], t0[v]);
     }
+#pragma unroll
+  for (int t = 0; t < TN * TM; t++) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);  // VALU
+  }
 }
 
 // Wait until at most N of this wave's vector-memory operations are in
@@ -201,11 +214,11 @@ __device__ __forceinline__ void wait_vm_barrier() {
 // reading `nxt2`.
 template <class C, int TN, int TM>
 __device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int wave, int p, int pend,
-                                              const char *cur, char *nxt2, int wn, int wm,
+                                              const char *cur, char *nxt2, int wn, int wm, int r16, int r8,
                                               float (&acc)[TN][TM][16]) {
   wait_vm_barrier<C::WPW>();
   dma_stage<C>(g, slots, wave, p + 2, pend, nxt2);
-  compute_stage<C, TN, TM>(cur, wn, wm, acc);
+  compute_stage<C, TN, TM>(cur, wn, wm, r16, r8, acc);
   // Keep each stage's MFMAs and folds inside the stage: interleaving them
   // with the next stage's only lengthens register lifetimes.
   __builtin_amdgcn_sched_barrier(0);
@@ -235,6 +248,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
 
   Slots<C> slots;
   init_slots<C>(g, wave, nt0, mt0, slots);
+  const int r16 = opaque(row * 16), r8 = opaque(row * 8);
   // Split z of the K range: block pairs [p0, pend).
   const int z = blockIdx.z;
   const int p0 = static_cast<int>(static_cast<long>(g.pp) * z / g.splits);
@@ -244,12 +258,12 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
   // Unrolled by three so every stage's buffer roles are static.
   int p = p0;
   for (; p + 2 < pend; p += 3) {
-    pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, acc);
-    pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, acc);
-    pipeline_step<C, TN, TM>(g, slots, wave, p + 2, pend, lds2, lds1, wn, wm, acc);
+    pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, r16, r8, acc);
+    pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, r16, r8, acc);
+    pipeline_step<C, TN, TM>(g, slots, wave, p + 2, pend, lds2, lds1, wn, wm, r16, r8, acc);
   }
-  if (p < pend) pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, acc);
-  if (p + 1 < pend) pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, acc);
+  if (p < pend) pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, r16, r8, acc);
+  if (p + 1 < pend) pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, r16, r8, acc);
   // Drain the prefetches of stages past pend before the workgroup can exit
   // (their LDS must not be written after it is released).
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
@@ -355,24 +369,12 @@ hipError_t launch_cfg(GemmArgs g, int splits, float *part, hipStream_t st) {
 
 }  // namespace
 
-// Workgroup tile by batch size: 128 rows x 32 / 64 tokens for small batches
-// and up to M = 768 (more, smaller workgroups keep two or more resident per
-// CU), 128 x 128 above (operand reuse wins once every CU holds several).
-// Long K (> 8192) keeps 128 x 128: split K then supplies the workgroups.
-enum class GemmCfg { k128x32, k128x64, k128x128 };
-static GemmCfg gemm_cfg(size_t m, size_t pp) {
-  if (m > 32 && m <= 64) return GemmCfg::k128x64;
-  return (m <= 32 || (m <= 768 && pp <= 128)) ? GemmCfg::k128x32 : GemmCfg::k128x128;
-}
-
-int plan_q4_gemm_splits(const lgh_q4 *w, size_t m) {
-  const size_t mt = (m + 31) / 32;
-  switch (gemm_cfg(m, w->pp)) {
-    case GemmCfg::k128x32: return splits_for<4, 1, 1, 1>(w->nt, mt, w->pp);
-    case GemmCfg::k128x64: return splits_for<4, 1, 1, 2>(w->nt, mt, w->pp);
-    default: return splits_for<2, 2, 2, 2>(w->nt, mt, w->pp);
-  }
-}
+// Workgroup tile 128 rows x 32 tokens (4 waves, one 32 x 32 tile each): at
+// every prefill shape measured (M = 512 / 2048, K = 2048 / 10752) it is as
+// fast as or faster than 128 x 64 and 128 x 128 -- the inner loop is bound by
+// the matrix core plus the fold (which do not overlap on gfx950), and the
+// small tile keeps the most workgroups resident to cover the stage loads.
+int plan_q4_gemm_splits(const lgh_q4 *w, size_t m) { return splits_for<4, 1, 1, 1>(w->nt, (m + 31) / 32, w->pp); }
 
 hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t m, int mode, float *part,
                           size_t part_floats, hipStream_t st) {
@@ -394,11 +396,7 @@ hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t 
              1,
              static_cast<uint32_t>(w->nt * w->pp * kMxWRec),
              static_cast<uint32_t>(mt * w->pp * kMxARec)};
-  switch (gemm_cfg(m, w->pp)) {
-    case GemmCfg::k128x32: return launch_cfg<4, 1, 1, 1>(g, splits, part, st);
-    case GemmCfg::k128x64: return launch_cfg<4, 1, 1, 2>(g, splits, part, st);
-    default: return launch_cfg<2, 2, 2, 2>(g, splits, part, st);
-  }
+  return launch_cfg<4, 1, 1, 1>(g, splits, part, st);
 }
 
 hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const uint8_t *mxa, size_t m, int32_t *out,

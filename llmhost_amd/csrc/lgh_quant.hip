@@ -243,28 +243,58 @@ __device__ __forceinline__ void store_hl_group8(uint8_t *rec, int s, int tok, ui
 }
 
 // Activations: one 8-lane group per (token, block) over the padded ranges
-// [0, 32*mt) x [0, 2*pp), blocks fastest so x is read contiguously.
+// [0, 32*mt) x [0, 2*pp), blocks fastest so x is read contiguously.  Each
+// group handles kActJobs of them, `stride` groups apart, with every x load
+// issued before the first is used.  The h / l E3M2 codes of each int8 code
+// come from a 256-entry LDS table built per workgroup (q + 128 ->
+// code(h) | code(l) << 6), a lookup in place of ~25 VALU per code.
+constexpr int kActJobs = 2;
+
 __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, int m, int bpr,
                                                                 int pp, int per_row,
-                                                                const float *row_scale, size_t groups,
-                                                                uint8_t *mxa) {
-  const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
-  if (gi >= groups) return;  // whole 8-lane groups exit together
+                                                                const float *row_scale, uint32_t groups,
+                                                                uint32_t stride, uint8_t *mxa) {
+  __shared__ uint16_t s_hl[256];
+  static_assert(kThreads == 256, "one table entry per thread");
+  {
+    int h, l;
+    split_h_l(static_cast<int>(threadIdx.x) - 128, h, l);
+    s_hl[threadIdx.x] = static_cast<uint16_t>(e3m2_code(h) | (e3m2_code(l) << 6));
+  }
+  const uint32_t g0 = (blockIdx.x * kThreads + threadIdx.x) >> 3;
   const int g = threadIdx.x & 7;
-  const int t = static_cast<int>(gi / (2 * pp)), b = static_cast<int>(gi % (2 * pp));
-  const bool ok = t < m && b < bpr;
-  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (ok) v = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
-  const bool pr = ok && per_row;
-  const float rs = pr ? row_scale[t] : 0.0f;
-  float scale;
-  int sum;
-  const int q = act_quant_group8(v, pr, rs, scale, sum);
-  uint32_t vh, vl;
-  codes24_hl(q, vh, vl);
-  uint8_t *rec = mxa + (static_cast<size_t>(t >> 5) * pp + (b >> 1)) * kMxARec;
-  store_hl_group8(rec, b & 1, t & 31, vh, vl);
-  if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = ok ? scale : 0.0f;
+  const uint32_t bp2 = 2u * static_cast<uint32_t>(pp);
+  float4 v[kActJobs];
+#pragma unroll
+  for (int j = 0; j < kActJobs; j++) {
+    const uint32_t gi = g0 + j * stride;
+    const int t = static_cast<int>(gi / bp2), b = static_cast<int>(gi % bp2);
+    v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (gi < groups && t < m && b < bpr) v[j] = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kActJobs; j++) {
+    const uint32_t gi = g0 + j * stride;
+    if (gi >= groups) break;  // uniform across each 8-lane group
+    const int t = static_cast<int>(gi / bp2), b = static_cast<int>(gi % bp2);
+    const bool ok = t < m && b < bpr;
+    const bool pr = ok && per_row;
+    const float rs = pr ? row_scale[t] : 0.0f;
+    float scale;
+    int sum;
+    const int q = act_quant_group8(v[j], pr, rs, scale, sum);
+    uint32_t vh = 0, vl = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t hl = s_hl[(q >> (8 * i)) + 128 & 255];
+      vh |= (hl & 63u) << (6 * i);
+      vl |= (hl >> 6) << (6 * i);
+    }
+    uint8_t *rec = mxa + (static_cast<size_t>(t >> 5) * pp + (b >> 1)) * kMxARec;
+    store_hl_group8(rec, b & 1, t & 31, vh, vl);
+    if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = ok ? scale : 0.0f;
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__restrict__ aq, int m, int bpr,
@@ -333,10 +363,12 @@ hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const size_t groups = mt * 32 * pp * 2;
-  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x,
-                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale, groups,
-                     mxa);
+  const size_t groups = mt * 32 * pp * 2;  // < 2^31: the image is below kMxMaxBytes
+  const unsigned wgs = blocks_for((groups + kActJobs - 1) / kActJobs * 8, kThreads);
+  const uint32_t stride = wgs * (kThreads / 8);
+  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(wgs), dim3(kThreads), 0, st, x, static_cast<int>(m),
+                     static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale,
+                     static_cast<uint32_t>(groups), stride, mxa);
   return hipGetLastError();
 }
 
