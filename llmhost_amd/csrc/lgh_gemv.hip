@@ -148,16 +148,17 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   // (3) x -> LDS codes.
   quantize_regs_to_lds<THREADS, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
 
-  // (4) dots + fold.
+  // (4) dots + fold, branch-free so every LDS read is issued before the
+  // weights arrive: a block past the row has zero nibbles and a zero scale
+  // (out-of-range loads) and reads block 0's codes, so it adds exactly 0.
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < BPL; j++) {
     const int kb = kb0 + 16 * j;
-    if (kb < bpr) {
-      const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kb * 32);
-      const int d = dot_q4_block16(w[j], ap[0], ap[1]);
-      acc = fmaf(static_cast<float>(d), h2f(s[j]) * s_sa[kb], acc);
-    }
+    const int kbc = kb < bpr ? kb : 0;
+    const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kbc * 32);
+    const int d = dot_q4_block16(w[j], ap[0], ap[1]);
+    acc = fmaf(static_cast<float>(d), h2f(s[j]) * s_sa[kbc], acc);
   }
   // (5) 16-lane row sums (every lane of a DPP row ends with its row's sum).
   acc += dpp<0xB1>(acc);   // quad_perm [1,0,3,2]
@@ -258,24 +259,23 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
 #pragma unroll
   for (int j = 0; j < BPL; j++) {
     const int kb = kb0 + 16 * j;
-    if (kb < bpr) {
-      const int u[8] = {nib_lo16(w[j].x), nib_hi16(w[j].x), nib_lo16(w[j].y), nib_hi16(w[j].y),
-                        nib_lo16(w[j].z), nib_hi16(w[j].z), nib_lo16(w[j].w), nib_hi16(w[j].w)};
-      const float sw = h2f(s[j]);
+    const int kbc = kb < bpr ? kb : 0;  // past the row: zero weights and scale, adds exactly 0
+    const int u[8] = {nib_lo16(w[j].x), nib_hi16(w[j].x), nib_lo16(w[j].y), nib_hi16(w[j].y),
+                      nib_lo16(w[j].z), nib_hi16(w[j].z), nib_lo16(w[j].w), nib_hi16(w[j].w)};
+    const float sw = h2f(s[j]);
 #pragma unroll
-      for (int t = 0; t < T; t++) {
-        const v4i *ap = reinterpret_cast<const v4i *>(&s_qs[t][kb * 32]);
-        const v4i a0 = ap[0], a1 = ap[1];
-        int d = sdot4(u[0], a0.x, 0);
-        d = sdot4(u[1], a0.y, d);
-        d = sdot4(u[2], a0.z, d);
-        d = sdot4(u[3], a0.w, d);
-        d = sdot4(u[4], a1.x, d);
-        d = sdot4(u[5], a1.y, d);
-        d = sdot4(u[6], a1.z, d);
-        d = sdot4(u[7], a1.w, d);
-        acc[t] = fmaf(static_cast<float>(d), sw * s_sa[t][kb], acc[t]);
-      }
+    for (int t = 0; t < T; t++) {
+      const v4i *ap = reinterpret_cast<const v4i *>(&s_qs[t][kbc * 32]);
+      const v4i a0 = ap[0], a1 = ap[1];
+      int d = sdot4(u[0], a0.x, 0);
+      d = sdot4(u[1], a0.y, d);
+      d = sdot4(u[2], a0.z, d);
+      d = sdot4(u[3], a0.w, d);
+      d = sdot4(u[4], a1.x, d);
+      d = sdot4(u[5], a1.y, d);
+      d = sdot4(u[6], a1.z, d);
+      d = sdot4(u[7], a1.w, d);
+      acc[t] = fmaf(static_cast<float>(d), sw * s_sa[t][kbc], acc[t]);
     }
   }
   // (5) row sums, slices in order, epilogue per token.
@@ -569,14 +569,13 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(Q8GemvArgs a) {
 #pragma unroll
   for (int st = 0; st < S; st++) {
     const int kb = st * kWave + lane;
-    if (kb < bpr) {
-      const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kb * 32);
-      const v4i a0 = ap[0], a1 = ap[1];
-      const float sa = s_sa[kb];
+    const int kbc = kb < bpr ? kb : 0;  // past the row: zero weights and scale, adds exactly 0
+    const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kbc * 32);
+    const v4i a0 = ap[0], a1 = ap[1];
+    const float sa = s_sa[kbc];
 #pragma unroll
-      for (int r = 0; r < R; r++)
-        acc[r] = fmaf(static_cast<float>(dot_q8_block(w0[st][r], w1[st][r], a0, a1)), h2f(s[st][r]) * sa, acc[r]);
-    }
+    for (int r = 0; r < R; r++)
+      acc[r] = fmaf(static_cast<float>(dot_q8_block(w0[st][r], w1[st][r], a0, a1)), h2f(s[st][r]) * sa, acc[r]);
   }
   float *y = a.y + static_cast<size_t>(tok) * a.n;
 #pragma unroll
