@@ -12,7 +12,8 @@ weights) + 4*K (x) + 4*N (y) per GEMV.
 
 Also reported (one JSON line, under "extra"): the 16-layer decode sweep,
 ragged Q4 GEMM M in {4,16,64}, prefill Q4 GEMM M=512 / 2048 TOPS (fraction of
-int8 MFMA peak), Q8_0 GEMV K=N=1536 -- and, on rank 0, the CPU baseline: the
+int8 MFMA peak), Q8_0 GEMV K=N=1536, the tied heads, the decode FFN block
+(fused vs per-op) -- and, on rank 0, the CPU baseline: the
 oracle's runtime-dispatched llm-cpu restatement (VNNI-512 > AVX2 > scalar)
 timed on this host's cores over a bounded sample of the same GEMV workload.
 
@@ -224,6 +225,55 @@ def q4_head_case(gb: GpuBench, iters, n=65536, k=1536):
             "frac_hbm": q4_bytes(n, k) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def ffn_case(gb: GpuBench, iters, dim=1536, inter=8192):
+    """Decode FFN residual block (lfm2.rs:883-911), one token: the fused two-launch entry point
+    against the same math composed from the per-op entry points (torch for RMSNorm and
+    silu * u).  Rotating weight sets > 2x MALL."""
+    torch, q4 = gb.torch, gb.q4
+    import torch.nn.functional as F
+    from llmhost_amd import synth
+
+    set_bytes = 2 * inter * (dim // 32) * 18 + dim * (inter // 32) * 18
+    count = math.ceil(2 * MALL_BYTES / set_bytes)
+    raws = [torch.from_numpy(synth.q4_blocks(600 + j, n, k).view(np.uint8).copy()).cuda()
+            for j, (n, k) in enumerate([(inter, dim), (inter, dim), (dim, inter)])]
+    sets = [[q4.Q4Matrix.from_blocks(n, k, raws[j], gb.ctx)
+             for j, (n, k) in enumerate([(inter, dim), (inter, dim), (dim, inter)])] for _ in range(count)]
+    del raws
+    hidden = torch.from_numpy(synth.normal_f32(610, dim)).cuda()
+    nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(611, dim)).astype(np.float32)).cuda()
+    g = torch.zeros(inter, device="cuda")
+    u = torch.zeros(inter, device="cuda")
+
+    def fused(i):
+        w1, w3, w2 = sets[i % count]
+        q4.ffn_residual(w1, w3, w2, nw, 1e-5, hidden)
+
+    def unfused(i):
+        w1, w3, w2 = sets[i % count]
+        normed = nw * (hidden * torch.rsqrt((hidden.double() ** 2).mean() + 1e-5).float())
+        q4.gemv_q4_pair(w1, w3, normed, g, u)
+        h = F.silu(g) * u
+        q4.gemv_q4_add(w2, h, hidden)
+
+    def gemvs_only(i):  # the per-op path's two GEMV launches alone (no norm, no silu)
+        w1, w3, w2 = sets[i % count]
+        q4.gemv_q4_pair(w1, w3, hidden, g, u)
+        q4.gemv_q4_add(w2, g, hidden)
+
+    ms_f = gb.timed(fused, iters, 5)
+    ms_u = gb.timed(unfused, iters, 5)
+    ms_g = gb.timed(gemvs_only, iters, 5)
+    for ws in sets:
+        for w in ws:
+            w.free()
+    byts = set_bytes + 4 * dim * 3 + 4 * dim
+    return {"dim": dim, "inter": inter, "us": ms_f * 1e3, "gbs": byts / (ms_f * 1e-3) / 1e9,
+            "frac_hbm": byts / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "unfused_us": ms_u * 1e3,
+            "pair_and_down_gemvs_only_us": ms_g * 1e3,
+            "bytes": byts, "launches": 2}
+
+
 def cpu_baseline(target_s: float = 12.0):
     """The oracle's llm-cpu restatement (runtime-dispatched kernel, pinned
     pool) on this host, over rotating packed copies larger than the LLC."""
@@ -359,6 +409,8 @@ def main():
         log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
         extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
         extra["q4_head_k1536_n65536"] = q4_head_case(gb, 20)
+        log("[bench] decode FFN block (fused vs per-op)")
+        extra["ffn_block_dim1536_inter8192"] = ffn_case(gb, 100)
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")

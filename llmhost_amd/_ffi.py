@@ -66,6 +66,9 @@ SIGNATURES = {
     "lgh_q4_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q8_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q4_mfma_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
+    "lgh_q4_ffn_residual": (_I, [_P, _P, _P, _P, _P, C.c_float, _P]),
+    "lgh_q4_ffn_residual_dev": (_I, [_P, _P, _P, _P, _P, C.c_float, _P]),
+    "lgh_q4_ffn_gate_up": (_I, [_P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _P, _P]),
 }
 
 _lib = None

@@ -192,6 +192,7 @@ void lgh_destroy(lgh_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->stage) (void)hipFree(ctx->stage);
+  if (ctx->ffn) (void)hipFree(ctx->ffn);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
 }
@@ -515,6 +516,99 @@ int lgh_q4_gemv_pair(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const flo
   if (int r = lgh_q4_gemv_pair_dev(ctx, wg, wu, xd, gd, ud)) return r;
   LGH_HIP(ctx, hipMemcpyAsync(y_gate, gd, yb, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipMemcpyAsync(y_up, ud, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+// ---- decode FFN block ---------------------------------------------------
+static int check_ffn(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2) {
+  if (!w1 || !w3) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (w1->k != w3->k || w1->n != w3->n)
+    return fail(ctx, LGH_ERR_SHAPE, "gate/up need equal shapes: %zux%zu, %zux%zu", w1->n, w1->k, w3->n, w3->k);
+  if (w2 && (w2->k != w1->n || w2->n != w1->k))
+    return fail(ctx, LGH_ERR_SHAPE, "down must be %zux%zu, got %zux%zu", w1->k, w1->n, w2->n, w2->k);
+  if (w1->n % 32 != 0) return fail(ctx, LGH_ERR_SHAPE, "intermediate size %zu is not a multiple of 32", w1->n);
+  if (w1->bpr > lgh::kFfnMaxBpr)
+    return fail(ctx, LGH_ERR_SHAPE, "hidden size %zu exceeds %zu", w1->k, lgh::kFfnMaxBpr * 32);
+  return LGH_OK;
+}
+
+int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
+                            const float *norm_w_dev, float eps, float *hidden_dev) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_ffn(ctx, w1, w3, w2)) return r;
+  if (w1->k == 0 || w1->n == 0) return LGH_OK;  // no hidden elements, or W2 h = 0 (hidden + 0 is hidden)
+  if (!hidden_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
+  if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "hidden and norm weight must be 16-byte aligned");
+  if (int r = set_device(ctx)) return r;
+  const size_t n = w1->n;
+  // PerBlock and a GEMV-sized W2: h leaves the gate/up kernel already
+  // quantized.  Otherwise (PerRow needs all of h for its scale, or K beyond
+  // the GEMV) h goes out in f32 through the regular M = 1 path.
+  const bool codes = ctx->act_mode == LGH_ACT_PER_BLOCK && lgh::plan_q4_gemv(w2->n, w2->bpr, 1).ok;
+  Carve cv;
+  const size_t o_q = cv.take(n), o_s = cv.take(n / 32 * sizeof(float)), o_f = cv.take(codes ? 0 : n * sizeof(float));
+  if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, cv.off)) return r;
+  char *f = static_cast<char *>(ctx->ffn);
+  auto *hq = reinterpret_cast<int8_t *>(f + o_q);
+  auto *hs = reinterpret_cast<float *>(f + o_s);
+  auto *hf = reinterpret_cast<float *>(f + o_f);
+  LGH_HIP(ctx, lgh::launch_ffn_gate_up(w1, w3, hidden_dev, norm_w_dev, eps, ctx->act_mode, codes ? hq : nullptr, hs,
+                                       codes ? nullptr : hf, nullptr, nullptr, ctx->stream));
+  if (!codes) return lgh_q4_gemm_dev(ctx, w2, hf, hidden_dev, 1, LGH_ADD_F64);
+  LGH_HIP(ctx, lgh::launch_q4_gemv_codes(w2, hq, hs, hidden_dev, LGH_ADD_F64, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2, const float *norm_w,
+                        float eps, float *hidden) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_ffn(ctx, w1, w3, w2)) return r;
+  if (w1->k == 0 || w1->n == 0) return LGH_OK;
+  if (!hidden) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = w1->k * sizeof(float);
+  const size_t ox = cv.take(xb), on = cv.take(norm_w ? xb : 0);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *nd = norm_w ? reinterpret_cast<float *>(st + on) : nullptr;
+  LGH_HIP(ctx, hipMemcpyAsync(xd, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (norm_w) LGH_HIP(ctx, hipMemcpyAsync(nd, norm_w, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q4_ffn_residual_dev(ctx, w1, w3, w2, nd, eps, xd)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(hidden, xd, xb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_ffn_gate_up(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const float *norm_w, float eps,
+                       const float *hidden, float *g, float *u, float *h, int8_t *hq, float *hs) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (int r = check_ffn(ctx, w1, w3, nullptr)) return r;
+  if (w1->k == 0 || w1->n == 0) return LGH_OK;
+  if (!hidden || !g || !u || !h) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/g/u/h");
+  if (int r = set_device(ctx)) return r;
+  const size_t n = w1->n, xb = w1->k * sizeof(float), yb = n * sizeof(float);
+  Carve cv;
+  const size_t ox = cv.take(xb), on = cv.take(norm_w ? xb : 0), og = cv.take(yb), ou = cv.take(yb),
+               oh = cv.take(yb), oq = cv.take(n), os = cv.take(n / 32 * sizeof(float));
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *nd = norm_w ? reinterpret_cast<float *>(st + on) : nullptr;
+  float *gd = reinterpret_cast<float *>(st + og), *ud = reinterpret_cast<float *>(st + ou);
+  float *hd = reinterpret_cast<float *>(st + oh), *sd = reinterpret_cast<float *>(st + os);
+  auto *qd = reinterpret_cast<int8_t *>(st + oq);
+  LGH_HIP(ctx, hipMemcpyAsync(xd, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (norm_w) LGH_HIP(ctx, hipMemcpyAsync(nd, norm_w, xb, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_ffn_gate_up(w1, w3, xd, nd, eps, ctx->act_mode, qd, sd, hd, gd, ud, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(g, gd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(u, ud, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(h, hd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  if (hq) LGH_HIP(ctx, hipMemcpyAsync(hq, qd, n, hipMemcpyDeviceToHost, ctx->stream));
+  if (hs) LGH_HIP(ctx, hipMemcpyAsync(hs, sd, n / 32 * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return LGH_OK;
 }

@@ -5,6 +5,8 @@
 
 #include <cstdint>
 
+#include "../../include/llm_gpu_hip.h"
+
 namespace lgh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -240,6 +242,60 @@ __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float ro
   s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xf, 0xf, false);
   sum = s;
   return (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (static_cast<int>(static_cast<uint32_t>(q3) << 24));
+}
+
+// ---- x -> LDS codes, shared by the GEMV-style kernels --------------------
+// Quantize the float4s held in registers (thread t holds x4[t + THREADS j])
+// into LDS: s_qs (natural order) and s_sa, for blocks [0, nblk).  All
+// threads must call it; it ends with a barrier.
+template <int THREADS, int XJ>
+__device__ __forceinline__ void quant_regs(const float4 (&xv)[XJ], int nblk, bool per_row, float row_scale,
+                                           int8_t *s_qs, float *s_sa) {
+  const int tid = threadIdx.x;
+  const int g = tid & 7;
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int b = (tid >> 3) + j * (THREADS / 8);
+    if (b < nblk) {  // uniform across each 8-lane group
+      float scale;
+      int sum;
+      const int q = act_quant_group8(xv[j], per_row, row_scale, scale, sum);
+      reinterpret_cast<int *>(s_qs)[b * 8 + g] = q;
+      if (g == 0) s_sa[b] = scale;
+    }
+  }
+  __syncthreads();
+}
+
+// Row amax / 127 over the register-resident x (PerRow), or 0.
+template <int THREADS, int XJ>
+__device__ __forceinline__ float row_scale_of(const float4 (&xv)[XJ], int per_row, float *s_red) {
+  if (!per_row) return 0.0f;
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < XJ; j++)
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[j].x), fabsf(xv[j].y)), fmaxf(fabsf(xv[j].z), fabsf(xv[j].w))));
+  m = wave_max(m);
+  if ((threadIdx.x & (kWave - 1)) == 0) s_red[threadIdx.x / kWave] = m;
+  __syncthreads();
+  m = 0.0f;
+  for (int w = 0; w < THREADS / kWave; w++) m = fmaxf(m, s_red[w]);
+  return div127_rn(m);
+}
+
+template <int THREADS, int XJ>
+__device__ __forceinline__ void quantize_regs_to_lds(const float4 (&xv)[XJ], int bpr, int per_row, int8_t *s_qs,
+                                                     float *s_sa, float *s_red) {
+  const float rs = row_scale_of<THREADS, XJ>(xv, per_row, s_red);
+  quant_regs<THREADS, XJ>(xv, bpr, per_row != 0, rs, s_qs, s_sa);
+}
+
+__device__ __forceinline__ void store_row(float *y, int row, float acc16, int mode) {
+  const float v = acc16 * 0.0625f;  // exact: undo the x16 of the nibble unpack
+  if (mode == LGH_ADD_F64)
+    y[row] = static_cast<float>(static_cast<double>(y[row]) + static_cast<double>(v));
+  else
+    y[row] = v;
 }
 
 // ---- MX-fp6 operand codes ----------------------------------------------------

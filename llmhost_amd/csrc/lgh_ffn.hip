@@ -1,0 +1,188 @@
+// Decode-step SwiGLU FFN residual block for gfx950, one token (replaces
+// Lfm2::ffn_residual_in, crates/llm-engine/src/lfm2.rs:883-911):
+//   normed = rms_norm(hidden, ffn_norm)          crates/llm-cpu/src/ops.rs:8-23
+//   g, u   = W1 normed, W3 normed                gemv_q4_pair, gemv_q4.rs:396-443
+//   h      = silu(g) * u                         ops.rs:27-36, lfm2.rs:902-905
+//   hidden = f32(f64(hidden) + f64(W2 h))        gemv_q4_add, gemv_q4.rs:356-363
+// in two launches instead of five passes:
+//   * ffn_gate_up_kernel: per workgroup, the norm of hidden (sum of squares in
+//     f64, as the reference), the ActQ8 codes of `normed` in LDS, 32 rows of
+//     W1 and the same 32 rows of W3 (the GEMV's mapping: one weight row per
+//     16-lane DPP row), then silu(g) * u for those 32 rows -- exactly one
+//     32-element block of h -- and that block's ActQ8 codes and scale;
+//   * the down GEMV reading those codes (q4_gemv_kernel, PREQ), AddF64 into
+//     hidden.
+// The down GEMV therefore skips loading 4*inter bytes of h and quantizing it
+// in every workgroup, which is the prologue that bounds the plain GEMV at
+// K = 8192.
+#include "lgh_device.h"
+#include "lgh_internal.h"
+
+namespace lgh {
+
+namespace {
+
+constexpr int kFfnWaves = 16;  // waves 0-7: 4 rows each of W1; waves 8-15: the same rows of W3
+constexpr int kFfnThreads = kFfnWaves * kWave;
+
+struct FfnUpArgs {
+  const uint8_t *qs1, *qs3;  // W1 (gate), W3 (up): nibble planes [n][bpr][16]
+  const uint16_t *sc1, *sc3;
+  const float *x;   // hidden [k]
+  const float *nw;  // norm weight [k], or null for no norm
+  float eps;
+  int bpr;        // k / 32
+  int per_row;    // ActQ8 mode for `normed`
+  int8_t *hq;     // ActQ8 (PerBlock) codes of h [n], or null
+  float *hs;      // their scales [n / 32]
+  float *hf;      // h [n], or null
+  float *g_out;   // g [n], or null
+  float *u_out;   // u [n], or null
+};
+
+template <int BPL>
+__global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
+  constexpr int KB = 16 * BPL;  // blocks covered (>= bpr)
+  constexpr int XJ = (KB * 8 + kFfnThreads - 1) / kFfnThreads;
+  __shared__ __align__(16) int8_t s_qs[KB * 32];
+  __shared__ float s_sa[KB];
+  __shared__ float s_red[kFfnWaves];
+  __shared__ double s_ss[kFfnWaves];
+  __shared__ float s_gu[2][32];
+  __shared__ __align__(16) float s_h[32];
+  const int bpr = a.bpr;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = uniform(tid / kWave);
+  const int mat = wave >> 3;  // 0: gate (W1), 1: up (W3)
+  const int base = blockIdx.x * 32;
+  const int row0 = base + (wave & 7) * 4;
+  const int r = lane >> 4, c = lane & 15;
+
+  // (1) hidden and the norm weight (elements >= k read as 0).
+  const auto xr = make_rsrc(a.x, static_cast<uint32_t>(bpr) * 128u);
+  const auto nr = make_rsrc(a.nw, a.nw ? static_cast<uint32_t>(bpr) * 128u : 0u);
+  float4 xv[XJ], nv[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * kFfnThreads) * 16u);
+    nv[j] = buf_load_f4(nr, static_cast<uint32_t>(tid + j * kFfnThreads) * 16u);
+  }
+
+  // (2) every weight load of this lane: 4 rows of W1 or W3, BPL blocks each.
+  const uint8_t *qs = mat ? a.qs3 : a.qs1;
+  const uint16_t *sc = mat ? a.sc3 : a.sc1;
+  const size_t blk0 = static_cast<size_t>(row0) * bpr;
+  const auto wr = make_rsrc(qs + blk0 * 16, static_cast<uint32_t>(4 * bpr) * 16u);
+  const auto sr = make_rsrc(sc + blk0, static_cast<uint32_t>(4 * bpr) * 2u);
+  uint4 w[BPL];
+  uint16_t s[BPL];
+#pragma unroll
+  for (int j = 0; j < BPL; j++) {
+    const int kb = c + 16 * j;
+    const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
+    w[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 16u : kOOB);
+    s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
+  }
+
+  // (3) RMSNorm (ops.rs:8-23): sum of squares in f64, scale =
+  // f32(1 / sqrt(sumsq * (1/dim) + eps)) in f64, normed = w * (x * scale) in
+  // f32.  The f64 sum is a fixed tree instead of the reference's sequence.
+  if (a.nw) {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < XJ; j++) {
+      const double x0 = xv[j].x, x1 = xv[j].y, x2 = xv[j].z, x3 = xv[j].w;
+      ss += x0 * x0;
+      ss += x1 * x1;
+      ss += x2 * x2;
+      ss += x3 * x3;
+    }
+    for (int off = kWave / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    if (lane == 0) s_ss[wave] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < kFfnWaves; i++) tot += s_ss[i];
+    const double inv_dim = 1.0 / static_cast<double>(bpr * 32);
+    const float scale = static_cast<float>(1.0 / sqrt(tot * inv_dim + static_cast<double>(a.eps)));
+#pragma unroll
+    for (int j = 0; j < XJ; j++) {
+      xv[j].x = nv[j].x * (xv[j].x * scale);
+      xv[j].y = nv[j].y * (xv[j].y * scale);
+      xv[j].z = nv[j].z * (xv[j].z * scale);
+      xv[j].w = nv[j].w * (xv[j].w * scale);
+    }
+  }
+
+  // (4) ActQ8 of normed into LDS, shared by both matrices.
+  quantize_regs_to_lds<kFfnThreads, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
+
+  // (5) dots + fold (branch-free: blocks past the row add exactly 0), DPP
+  // row sums, then g / u of the workgroup's 32 rows into LDS.
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < BPL; j++) {
+    const int kb = c + 16 * j;
+    const int kbc = kb < bpr ? kb : 0;
+    const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kbc * 32);
+    const int d = dot_q4_block16(w[j], ap[0], ap[1]);
+    acc = fmaf(static_cast<float>(d), h2f(s[j]) * s_sa[kbc], acc);
+  }
+  acc += dpp<0xB1>(acc);
+  acc += dpp<0x4E>(acc);
+  acc += dpp<0x141>(acc);
+  acc += dpp<0x140>(acc);
+  if (c == 0) s_gu[mat][(wave & 7) * 4 + r] = acc * 0.0625f;  // exact: undo the x16 of the unpack
+  __syncthreads();
+
+  // (6) h = silu(g) * u for the 32 rows (one ActQ8 block of h), its codes
+  // and scale (8 lanes, as act_quant_kernel).  One wave; s_h is written and
+  // read by the same wave.
+  if (wave == 0) {
+    if (lane < 32) {
+      const float g = s_gu[0][lane], u = s_gu[1][lane];
+      const float h = (g / (1.0f + expf(-g))) * u;
+      s_h[lane] = h;
+      if (a.g_out) a.g_out[base + lane] = g;
+      if (a.u_out) a.u_out[base + lane] = u;
+      if (a.hf) a.hf[base + lane] = h;
+    }
+    if (a.hq && lane < 8) {
+      const float4 hv = reinterpret_cast<const float4 *>(s_h)[lane];
+      float scale;
+      int sum;
+      const int q = act_quant_group8(hv, false, 0.0f, scale, sum);
+      reinterpret_cast<int *>(a.hq + base)[lane] = q;
+      if (lane == 0) a.hs[blockIdx.x] = scale;
+    }
+  }
+}
+
+template <int BPL>
+hipError_t launch_gate_up(const FfnUpArgs &a, int wgs, hipStream_t st) {
+  hipLaunchKernelGGL(ffn_gate_up_kernel<BPL>, dim3(wgs), dim3(kFfnThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool ffn_gate_up_supported(const lgh_q4 *w1) { return w1->bpr >= 1 && w1->bpr <= kFfnMaxBpr && w1->n % 32 == 0; }
+
+hipError_t launch_ffn_gate_up(const lgh_q4 *w1, const lgh_q4 *w3, const float *x, const float *norm_w, float eps,
+                              int per_row, int8_t *hq, float *hs, float *hf, float *g, float *u,
+                              hipStream_t st) {
+  if (!ffn_gate_up_supported(w1)) return hipErrorInvalidValue;
+  if (w1->n == 0) return hipSuccess;
+  const FfnUpArgs a{w1->qs, w3->qs, w1->sc, w3->sc, x, norm_w, eps, static_cast<int>(w1->bpr), per_row,
+                    hq, hs, hf, g, u};
+  const int wgs = static_cast<int>(w1->n / 32);
+  switch ((w1->bpr + 15) / 16) {
+    case 1: return launch_gate_up<1>(a, wgs, st);
+    case 2: return launch_gate_up<2>(a, wgs, st);
+    case 3: return launch_gate_up<3>(a, wgs, st);
+    default: return launch_gate_up<4>(a, wgs, st);
+  }
+}
+
+}  // namespace lgh

@@ -33,6 +33,8 @@ struct Q4GemvArgs {
   const uint16_t *sc1;
   float *y1;
   const float *x;
+  const int8_t *aq;  // PREQ: ActQ8 codes [k] and scales [k/32] instead of x
+  const float *as;
   int n;
   int bpr;
   int wgs0;  // workgroups covering matrix 0; the rest cover matrix 1
@@ -40,61 +42,11 @@ struct Q4GemvArgs {
   int per_row;
 };
 
-// Quantize the float4s held in registers (thread t holds x4[t + THREADS j])
-// into LDS: s_qs (natural order) and s_sa, for blocks [0, nblk).  All
-// threads must call it; it ends with a barrier.
-template <int THREADS, int XJ>
-__device__ __forceinline__ void quant_regs(const float4 (&xv)[XJ], int nblk, bool per_row, float row_scale,
-                                           int8_t *s_qs, float *s_sa) {
-  const int tid = threadIdx.x;
-  const int g = tid & 7;
-#pragma unroll
-  for (int j = 0; j < XJ; j++) {
-    const int b = (tid >> 3) + j * (THREADS / 8);
-    if (b < nblk) {  // uniform across each 8-lane group
-      float scale;
-      int sum;
-      const int q = act_quant_group8(xv[j], per_row, row_scale, scale, sum);
-      reinterpret_cast<int *>(s_qs)[b * 8 + g] = q;
-      if (g == 0) s_sa[b] = scale;
-    }
-  }
-  __syncthreads();
-}
-
-// Row amax / 127 over the register-resident x (PerRow), or 0.
-template <int THREADS, int XJ>
-__device__ __forceinline__ float row_scale_of(const float4 (&xv)[XJ], int per_row, float *s_red) {
-  if (!per_row) return 0.0f;
-  float m = 0.0f;
-#pragma unroll
-  for (int j = 0; j < XJ; j++)
-    m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[j].x), fabsf(xv[j].y)), fmaxf(fabsf(xv[j].z), fabsf(xv[j].w))));
-  m = wave_max(m);
-  if ((threadIdx.x & (kWave - 1)) == 0) s_red[threadIdx.x / kWave] = m;
-  __syncthreads();
-  m = 0.0f;
-  for (int w = 0; w < THREADS / kWave; w++) m = fmaxf(m, s_red[w]);
-  return div127_rn(m);
-}
-
-template <int THREADS, int XJ>
-__device__ __forceinline__ void quantize_regs_to_lds(const float4 (&xv)[XJ], int bpr, int per_row, int8_t *s_qs,
-                                                     float *s_sa, float *s_red) {
-  const float rs = row_scale_of<THREADS, XJ>(xv, per_row, s_red);
-  quant_regs<THREADS, XJ>(xv, bpr, per_row != 0, rs, s_qs, s_sa);
-}
-
-__device__ __forceinline__ void store_row(float *y, int row, float acc16, int mode) {
-  const float v = acc16 * 0.0625f;  // exact: undo the x16 of the nibble unpack
-  if (mode == LGH_ADD_F64)
-    y[row] = static_cast<float>(static_cast<double>(y[row]) + static_cast<double>(v));
-  else
-    y[row] = v;
-}
-
 // BPL blocks per lane and row, KW K slices, W waves; 4*(W/KW) rows per workgroup.
-template <int BPL, int KW, int W>
+// PREQ: the activations arrive already quantized (codes + scales, written by
+// the kernel that produced them), so the prologue is two short loads into
+// LDS instead of loading and quantizing x.
+template <int BPL, int KW, int W, bool PREQ>
 __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;  // blocks covered by the workgroup (>= bpr)
@@ -125,11 +77,25 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   const int r = lane >> 4, c = lane & 15;
   const int kb0 = ks * 16 * BPL + c;
 
-  // (1) x: bpr*8 float4s, XJ per thread.
-  const auto xr = make_rsrc(a.x, static_cast<uint32_t>(bpr) * 128u);
+  // (1) x: bpr*8 float4s, XJ per thread -- or (PREQ) the codes as 16-byte
+  // chunks and the block scales.
+  constexpr int QJ = PREQ ? (KB * 2 + THREADS - 1) / THREADS : 1;
+  constexpr int SJ = PREQ ? (KB + THREADS - 1) / THREADS : 1;
   float4 xv[XJ];
+  uint4 qv[QJ];
+  float sv[SJ];
+  if constexpr (PREQ) {
+    const auto qr = make_rsrc(a.aq, static_cast<uint32_t>(bpr) * 32u);
+    const auto ar = make_rsrc(a.as, static_cast<uint32_t>(bpr) * 4u);
 #pragma unroll
-  for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+    for (int j = 0; j < QJ; j++) qv[j] = buf_load16(qr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+#pragma unroll
+    for (int j = 0; j < SJ; j++) sv[j] = buf_load_f32(ar, static_cast<uint32_t>(tid + j * THREADS) * 4u);
+  } else {
+    const auto xr = make_rsrc(a.x, static_cast<uint32_t>(bpr) * 128u);
+#pragma unroll
+    for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+  }
 
   // (2) every weight load of this lane (rows past n fall outside the resource).
   const size_t blk0 = static_cast<size_t>(row0) * bpr;
@@ -145,8 +111,22 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
   }
 
-  // (3) x -> LDS codes.
-  quantize_regs_to_lds<THREADS, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
+  // (3) x -> LDS codes (chunks and scales past the row load as 0).
+  if constexpr (PREQ) {
+#pragma unroll
+    for (int j = 0; j < QJ; j++) {
+      const int i = tid + j * THREADS;
+      if (i < KB * 2) reinterpret_cast<uint4 *>(s_qs)[i] = qv[j];
+    }
+#pragma unroll
+    for (int j = 0; j < SJ; j++) {
+      const int i = tid + j * THREADS;
+      if (i < KB) s_sa[i] = sv[j];
+    }
+    __syncthreads();
+  } else {
+    quantize_regs_to_lds<THREADS, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
+  }
 
   // (4) dots + fold, branch-free so every LDS read is issued before the
   // weights arrive: a block past the row has zero nibbles and a zero scale
@@ -179,9 +159,9 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   }
 }
 
-template <int BPL, int KW, int W>
+template <int BPL, int KW, int W, bool PREQ = false>
 hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
-  hipLaunchKernelGGL((q4_gemv_kernel<BPL, KW, W>), dim3(total_wgs), dim3(W * kWave), 0, st, a);
+  hipLaunchKernelGGL((q4_gemv_kernel<BPL, KW, W, PREQ>), dim3(total_wgs), dim3(W * kWave), 0, st, a);
   return hipGetLastError();
 }
 
@@ -613,6 +593,16 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat) {
 
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x, int mode,
                           int per_row, hipStream_t st) {
+  return launch_q4_gemv_any(w0, y0, w1, y1, x, nullptr, nullptr, mode, per_row, st);
+}
+
+hipError_t launch_q4_gemv_codes(const lgh_q4 *w, const int8_t *codes, const float *scales, float *y, int mode,
+                                hipStream_t st) {
+  return launch_q4_gemv_any(w, y, nullptr, nullptr, nullptr, codes, scales, mode, 0, st);
+}
+
+hipError_t launch_q4_gemv_any(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
+                              const int8_t *codes, const float *scales, int mode, int per_row, hipStream_t st) {
   if (w0->n == 0) return hipSuccess;
   const int nmat = w1 ? 2 : 1;
   const Q4GemvPlan p = plan_q4_gemv(w0->n, w0->bpr, nmat);
@@ -625,14 +615,18 @@ hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *
   a.sc1 = w1 ? w1->sc : nullptr;
   a.y1 = y1;
   a.x = x;
+  a.aq = codes;
+  a.as = scales;
   a.n = static_cast<int>(w0->n);
   a.bpr = static_cast<int>(w0->bpr);
   a.wgs0 = p.wgs_per_mat;
   a.mode = mode;
   a.per_row = per_row;
   const int total = p.wgs_per_mat * nmat;
-#define LGH_G16(BB, KK, WW) \
-  if (p.BPL == BB && p.KW == KK && p.W == WW) return launch_gemv16<BB, KK, WW>(a, total, st)
+  const bool preq = codes != nullptr;
+#define LGH_G16(BB, KK, WW)                                                                          \
+  if (p.BPL == BB && p.KW == KK && p.W == WW)                                                        \
+  return preq ? launch_gemv16<BB, KK, WW, true>(a, total, st) : launch_gemv16<BB, KK, WW, false>(a, total, st)
   LGH_G16(1, 1, 16);
   LGH_G16(1, 1, 8);
   LGH_G16(1, 1, 4);

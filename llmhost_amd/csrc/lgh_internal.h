@@ -51,6 +51,9 @@ struct lgh_ctx {
   // Device staging for the host-pointer entry points.
   void *stage = nullptr;
   size_t stage_bytes = 0;
+  // FFN block intermediates (h's codes / scales, or h in f32).
+  void *ffn = nullptr;
+  size_t ffn_bytes = 0;
 };
 
 struct lgh_q4 {
@@ -112,6 +115,23 @@ struct Q4GemvPlan {
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);
+// FFN gate/up stage of one decode token (lgh_ffn.hip): RMSNorm of x with
+// norm_w (null: none), ActQ8 (per_row mode) of the result, g = W1 normed and
+// u = W3 normed, h = silu(g) * u; writes the PerBlock ActQ8 codes hq [n] and
+// scales hs [n/32] of h when hq is not null, and h / g / u in f32 to hf / g /
+// u when those are not null.  W1, W3: n x k with n % 32 == 0, k <= 32 *
+// kFfnMaxBpr (one workgroup holds all of x's codes).
+constexpr size_t kFfnMaxBpr = 64;
+bool ffn_gate_up_supported(const lgh_q4 *w1);
+hipError_t launch_ffn_gate_up(const lgh_q4 *w1, const lgh_q4 *w3, const float *x, const float *norm_w, float eps,
+                              int per_row, int8_t *hq, float *hs, float *hf, float *g, float *u,
+                              hipStream_t stream);
+// The same GEMV on activations already quantized per block (ActQ8 PerBlock
+// codes [k] + scales [k/32], device pointers), e.g. by the FFN gate/up kernel.
+hipError_t launch_q4_gemv_codes(const lgh_q4 *w, const int8_t *codes, const float *scales, float *y, int mode,
+                                hipStream_t stream);
+hipError_t launch_q4_gemv_any(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
+                              const int8_t *codes, const float *scales, int mode, int per_row, hipStream_t stream);
 // Batched GEMV for 2 <= m <= 4 rows of x, quantized inside the kernel
 // (one launch).  ok is false when the shape does not fit.
 struct Q4BatchPlan {

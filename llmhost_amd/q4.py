@@ -340,6 +340,42 @@ def gemv_q4_pair(w_gate: Q4Matrix, w_up: Q4Matrix, x, out_gate, out_up) -> None:
                                      _np_ptr(out_up)))
 
 
+# ---- decode FFN block --------------------------------------------------------
+def ffn_residual(w1: Q4Matrix, w3: Q4Matrix, w2: Q4Matrix, norm_w, eps: float, hidden) -> None:
+    """Lfm2::ffn_residual_in for one token (crates/llm-engine/src/lfm2.rs:883-911): hidden +=
+    W2 (silu(W1 n) * W3 n) with n = rms_norm(hidden, norm_w, eps) (norm_w None: n = hidden);
+    the down projection is added in f64.  hidden is updated in place (numpy or torch)."""
+    ctx = w1.ctx
+    _shape_assert(w1.k == w3.k == w2.n and w1.n == w3.n == w2.k, "FFN shapes: W1, W3 [inter, dim], W2 [dim, inter]")
+    if _is_torch(hidden):
+        _shape_assert(hidden.numel() == w1.k, "hidden length != dim")
+        nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
+        ctx.check(lib().lgh_q4_ffn_residual_dev(ctx.handle, w1.handle, w3.handle, w2.handle, nw, float(eps),
+                                                _dev_ptr(hidden, "hidden")))
+        return
+    hidden = _host_f32(hidden, "hidden")
+    _shape_assert(hidden.size == w1.k, "hidden length != dim")
+    nw = None if norm_w is None else _np_ptr(_host_f32(norm_w, "norm_w"))
+    ctx.check(lib().lgh_q4_ffn_residual(ctx.handle, w1.handle, w3.handle, w2.handle, nw, float(eps),
+                                        _np_ptr(hidden)))
+
+
+def ffn_gate_up(w1: Q4Matrix, w3: Q4Matrix, norm_w, eps: float, hidden):
+    """The gate/up stage of ffn_residual alone (test hook): returns g, u, h = silu(g) * u and
+    h's PerBlock ActQ8 codes / scales as the down projection consumes them."""
+    ctx = w1.ctx
+    hidden = _host_f32(hidden, "hidden")
+    _shape_assert(hidden.size == w1.k, "hidden length != dim")
+    n = w1.n
+    g, u, h = (np.zeros(n, dtype=np.float32) for _ in range(3))
+    hq = np.zeros(n, dtype=np.int8)
+    hs = np.zeros(n // 32, dtype=np.float32)
+    nw = None if norm_w is None else _np_ptr(_host_f32(norm_w, "norm_w"))
+    ctx.check(lib().lgh_q4_ffn_gate_up(ctx.handle, w1.handle, w3.handle, nw, float(eps), _np_ptr(hidden),
+                                       _np_ptr(g), _np_ptr(u), _np_ptr(h), _np_ptr(hq), _np_ptr(hs)))
+    return g, u, h, hq, hs
+
+
 def q8_apply(m: Q8Matrix, x, tokens: int, out) -> None:
     """q8_apply (crates/llm-engine/src/weights.rs:194-227)."""
     ctx = m.ctx

@@ -69,6 +69,9 @@ def lib():
         L.oq_gemv_q4_pair.argtypes = [P, P, P, P, P, i, i, i]
         L.oq_gemm_q4.argtypes = [P, P, P, sz, i, i, i, i]
         L.oq_q8_apply.argtypes = [P, sz, sz, P, sz, P, i]
+        L.oq_rms_norm.argtypes = [P, P, sz, sz, C.c_float, P]
+        L.oq_silu_mul.argtypes = [P, P, sz]
+        L.oq_ffn_residual.argtypes = [P, P, P, P, C.c_float, P, i, i, i]
         L.oq_thread_range.argtypes = [sz, sz, sz, C.POINTER(sz), C.POINTER(sz)]
         L.oq_cpu_has.argtypes, L.oq_cpu_has.restype = [C.c_char_p], i
         _lib = L
@@ -231,6 +234,36 @@ def q8_apply(blocks: np.ndarray, n: int, k: int, x, tokens: int = 1, threads=1):
     assert x.size == tokens * k
     out = np.zeros((tokens, n) if tokens > 1 else (n,), dtype=np.float32)
     lib().oq_q8_apply(_p(blocks), n, k, _p(x), tokens, _p(out), threads)
+    return out
+
+
+def rms_norm(x, weight, eps: float):
+    """ops.rs:8-23 over the rows of x (row length = weight.size)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    weight = np.ascontiguousarray(weight, dtype=np.float32)
+    assert x.size % weight.size == 0
+    out = np.empty_like(x)
+    lib().oq_rms_norm(_p(x), _p(weight), weight.size, x.size // weight.size, eps, _p(out))
+    return out
+
+
+def silu_mul(g, u):
+    """silu(g) * u (ops.rs:27-36, lfm2.rs:902-905), f32."""
+    out = np.array(g, dtype=np.float32, copy=True)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    assert out.size == u.size
+    lib().oq_silu_mul(_p(out), _p(u), out.size)
+    return out
+
+
+def ffn_residual(w1: "Q4Matrix", w3: "Q4Matrix", w2: "Q4Matrix", norm_w, eps: float, hidden, per_row=False,
+                 kernel=KERNEL_DETECT, threads=1):
+    """Lfm2::ffn_residual_in (lfm2.rs:883-911) for one token; returns the new hidden."""
+    out = np.array(hidden, dtype=np.float32, copy=True)
+    assert out.size == w1.k == w3.k == w2.n and w1.n == w3.n == w2.k
+    nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
+    lib().oq_ffn_residual(w1.handle, w3.handle, w2.handle, None if nw is None else _p(nw), eps, _p(out),
+                          int(per_row), kernel, threads)
     return out
 
 

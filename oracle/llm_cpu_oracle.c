@@ -802,3 +802,45 @@ void oq_q8_apply(const oq_block_q8 *blocks, size_t n, size_t k, const float *x, 
     for_ranges((size_t)threads, n, q8_range, &j);
   }
 }
+
+/* ======================================================================
+ * Decode FFN block: rms_norm (llm-cpu/src/ops.rs:8-23), silu (ops.rs:27-36)
+ * and Lfm2::ffn_residual_in (llm-engine/src/lfm2.rs:883-911).
+ * ==================================================================== */
+void oq_rms_norm(const float *x, const float *weight, size_t dim, size_t rows, float eps, float *out) {
+  const double inv_dim = 1.0 / (double)dim;
+  for (size_t r = 0; r < rows; r++) {
+    const float *row = x + r * dim;
+    float *dst = out + r * dim;
+    double sumsq = 0.0;
+    for (size_t i = 0; i < dim; i++) sumsq += (double)row[i] * (double)row[i];
+    const float scale = (float)(1.0 / sqrt(sumsq * inv_dim + (double)eps));
+    for (size_t i = 0; i < dim; i++) dst[i] = weight[i] * (row[i] * scale);
+  }
+}
+
+void oq_silu_mul(float *g, const float *u, size_t n) {
+  for (size_t i = 0; i < n; i++) {
+    const float x = g[i];
+    g[i] = x / (1.0f + expf(-x));
+    g[i] *= u[i];
+  }
+}
+
+void oq_ffn_residual(const oq_q4_matrix *w1, const oq_q4_matrix *w3, const oq_q4_matrix *w2,
+                     const float *norm_w, float eps, float *hidden, int per_row, int kernel, int threads) {
+  const size_t dim = w1->k, inter = w1->n;
+  float *normed = malloc(dim * sizeof(float));
+  float *g = malloc(inter * sizeof(float));
+  float *u = malloc(inter * sizeof(float));
+  if (norm_w)
+    oq_rms_norm(hidden, norm_w, dim, 1, eps, normed);
+  else
+    memcpy(normed, hidden, dim * sizeof(float));
+  oq_gemv_q4_pair(w1, w3, normed, g, u, per_row, kernel, threads);
+  oq_silu_mul(g, u, inter);
+  oq_gemv_q4(w2, g, hidden, 1, per_row, kernel, threads);
+  free(normed);
+  free(g);
+  free(u);
+}

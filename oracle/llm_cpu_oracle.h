@@ -96,6 +96,18 @@ void oq_gemm_q4(const oq_q4_matrix *w, const float *x, float *out, size_t m, int
 void oq_q8_apply(const oq_block_q8 *blocks, size_t n, size_t k, const float *x,
                  size_t tokens, float *out, int threads);
 
+/* ---- decode FFN block (llm-cpu/src/ops.rs, llm-engine/src/lfm2.rs) ------ */
+/* rms_norm (ops.rs:8-23): rows of dim elements; f64 sequential sum of
+ * squares, scale = f32(1/sqrt(sumsq*(1/dim) + eps)) in f64, out = w*(x*scale). */
+void oq_rms_norm(const float *x, const float *weight, size_t dim, size_t rows, float eps, float *out);
+/* silu_inplace (ops.rs:27-36) on g, then g *= u (lfm2.rs:902-905). */
+void oq_silu_mul(float *g, const float *u, size_t n);
+/* Lfm2::ffn_residual_in (lfm2.rs:883-911) for one token: normed =
+ * rms_norm(hidden) (weight == NULL: normed = hidden), g, u = gemv_q4_pair,
+ * silu(g)*u, hidden = gemv_q4_add(w2, h). */
+void oq_ffn_residual(const oq_q4_matrix *w1, const oq_q4_matrix *w3, const oq_q4_matrix *w2,
+                     const float *norm_w, float eps, float *hidden, int per_row, int kernel, int threads);
+
 /* ---- pool (pool.rs:212-241 thread_range / for_ranges) ------------------ */
 void oq_thread_range(size_t tid, size_t nthreads, size_t n, size_t *start, size_t *end);
 int oq_max_threads(void); /* pool.rs:22 MAX_THREADS = 64 */

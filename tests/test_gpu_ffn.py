@@ -1,0 +1,122 @@
+"""GPU parity of the decode FFN block (lgh_q4_ffn_residual, the fused form of
+Lfm2::ffn_residual_in, crates/llm-engine/src/lfm2.rs:883-911) against the oracle.
+
+Stage by stage, because silu's exp on the GPU and in libm may differ in the last ulp, and a
+one-ulp change of h can move an ActQ8 code across a .5 tie:
+  * gate/up (test hook): g and u within the GEMV tolerance of the oracle's pair GEMV of the
+    oracle's rms_norm; h within 3 ulp-equivalents of silu(g) * u on the GPU's own g, u; h's
+    codes and scales bit-exact to ActQ8 of the GPU's own h;
+  * the whole block: hidden within the GEMV tolerance of hidden + W2 applied (oracle, AddF64)
+    to exactly those codes -- the second launch is the down projection of the first's output.
+"""
+
+import numpy as np
+import pytest
+
+from llmhost_amd import q4, synth
+
+from .conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1536, 8192), (96, 64), (544, 160), (2048, 256), (32, 32)]
+
+
+def _mats(ctx, oracle, dim, inter, seed):
+    b1 = synth.q4_blocks(seed, inter, dim)
+    b3 = synth.q4_blocks(seed + 1, inter, dim)
+    b2 = synth.q4_blocks(seed + 2, dim, inter)
+    gpu = [q4.Q4Matrix.from_blocks(inter, dim, b1, ctx), q4.Q4Matrix.from_blocks(inter, dim, b3, ctx),
+           q4.Q4Matrix.from_blocks(dim, inter, b2, ctx)]
+    cpu = [oracle.Q4Matrix(inter, dim, b1), oracle.Q4Matrix(inter, dim, b3), oracle.Q4Matrix(dim, inter, b2)]
+    return gpu, cpu
+
+
+def _inputs(dim, seed):
+    hidden = (synth.normal_f32(seed, dim) * np.float32(3.0)).astype(np.float32)
+    nw = (1 + 0.2 * synth.normal_f32(seed + 1, dim)).astype(np.float32)
+    return hidden, nw
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("dim,inter", SHAPES)
+def test_ffn_gate_up_stage(gpu_ctx, oracle, dim, inter, per_row):
+    (g1, g3, _), (c1, c3, _) = _mats(gpu_ctx, oracle, dim, inter, 10 + dim + inter)
+    hidden, nw = _inputs(dim, 20 + dim)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        g, u, h, hq, hs = q4.ffn_gate_up(g1, g3, nw, 1e-5, hidden)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    normed = oracle.rms_norm(hidden, nw, 1e-5)
+    rg, ru = oracle.gemv_q4_pair(c1, c3, normed, per_row=per_row, threads=8)
+    assert_close(g, rg, what="g")
+    assert_close(u, ru, what="u")
+    # h = silu(g) * u on the GPU's own g, u: four f32 roundings (exp, add, divide, multiply)
+    ref_h = oracle.silu_mul(g, u).astype(np.float64)
+    ulp = np.spacing(np.abs(ref_h).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(h.astype(np.float64) - ref_h) <= 4 * ulp + 1e-45)
+    # h's codes: ActQ8 (PerBlock) of the GPU's h, bit-exact
+    qs, sc, _ = oracle.act_quantize(h.reshape(1, -1), False)
+    assert np.array_equal(hq, qs.ravel())
+    assert np.array_equal(hs.view(np.uint32), sc.ravel().view(np.uint32))
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("dim,inter", SHAPES)
+def test_ffn_residual_block(gpu_ctx, oracle, dim, inter, norm):
+    (g1, g3, g2), (c1, c3, c2) = _mats(gpu_ctx, oracle, dim, inter, 30 + dim + inter)
+    hidden, nw = _inputs(dim, 40 + dim)
+    nw = nw if norm else None
+    _, _, _, hq, hs = q4.ffn_gate_up(g1, g3, nw, 1e-5, hidden)
+    got = hidden.copy()
+    q4.ffn_residual(g1, g3, g2, nw, 1e-5, got)
+    ref = oracle.gemv_q4_prep(c2, hq, hs, out=hidden.copy(), add=True, threads=8)
+    assert_close(got, ref, what="hidden")
+    # and the whole reference composition, up to the ties that an ulp of exp can move
+    full = oracle.ffn_residual(c1, c3, c2, nw, 1e-5, hidden, threads=8)
+    assert_close(got, full, atol=2e-2, rtol=1e-3, what="vs reference composition")
+
+
+def test_ffn_residual_per_row(gpu_ctx, oracle):
+    """PerRow: h leaves the first launch in f32 and the down GEMV quantizes it per row."""
+    dim, inter = 1536, 8192
+    (g1, g3, g2), (c1, c3, c2) = _mats(gpu_ctx, oracle, dim, inter, 50)
+    hidden, nw = _inputs(dim, 60)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow)
+    try:
+        _, _, h, _, _ = q4.ffn_gate_up(g1, g3, nw, 1e-5, hidden)
+        got = hidden.copy()
+        q4.ffn_residual(g1, g3, g2, nw, 1e-5, got)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    ref = oracle.gemv_q4(c2, h, out=hidden.copy(), add=True, per_row=True, threads=8)
+    assert_close(got, ref, what="hidden (PerRow)")
+
+
+def test_ffn_device_path_matches_host_path(gpu_ctx, oracle):
+    import torch
+
+    dim, inter = 1536, 8192
+    (g1, g3, g2), _ = _mats(gpu_ctx, oracle, dim, inter, 70)
+    hidden, nw = _inputs(dim, 80)
+    host = hidden.copy()
+    q4.ffn_residual(g1, g3, g2, nw, 1e-5, host)
+    dev = torch.from_numpy(hidden.copy()).cuda()
+    q4.ffn_residual(g1, g3, g2, torch.from_numpy(nw).cuda(), 1e-5, dev)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev.cpu().numpy(), host)
+
+
+def test_ffn_shape_errors(gpu_ctx):
+    b = synth.q4_blocks(1, 64, 4096)
+    big1 = q4.Q4Matrix.from_blocks(64, 4096, b, gpu_ctx)
+    big3 = q4.Q4Matrix.from_blocks(64, 4096, b, gpu_ctx)
+    big2 = q4.Q4Matrix.from_blocks(4096, 64, synth.q4_blocks(2, 4096, 64), gpu_ctx)
+    with pytest.raises(Exception, match="exceeds"):
+        q4.ffn_residual(big1, big3, big2, None, 0.0, np.zeros(4096, np.float32))
+    w1 = q4.Q4Matrix.from_blocks(64, 96, synth.q4_blocks(3, 64, 96), gpu_ctx)
+    w3 = q4.Q4Matrix.from_blocks(32, 96, synth.q4_blocks(4, 32, 96), gpu_ctx)
+    w2 = q4.Q4Matrix.from_blocks(96, 64, synth.q4_blocks(5, 96, 64), gpu_ctx)
+    with pytest.raises(Exception):
+        q4.ffn_residual(w1, w3, w2, None, 0.0, np.zeros(96, np.float32))
