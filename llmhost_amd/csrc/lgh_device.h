@@ -90,6 +90,31 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// The same wave64 sum for f64 (each DPP move is two 32-bit moves).
+template <int Ctrl>
+__device__ __forceinline__ double dpp64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b & 0xffffffffu), Ctrl, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), Ctrl, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                        static_cast<uint32_t>(lo));
+}
+
+__device__ __forceinline__ double readlane64(double v, int lane) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b & 0xffffffffu), lane));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ double wave_sum_dpp64(double v) {
+  v += dpp64<0xB1>(v);
+  v += dpp64<0x4E>(v);
+  v += dpp64<0x141>(v);
+  v += dpp64<0x140>(v);
+  return (readlane64(v, 0) + readlane64(v, 16)) + (readlane64(v, 32) + readlane64(v, 48));
+}
+
 // f16 bits -> f32, exact (v_cvt_f32_f16; every binary16 value is a binary32
 // value), matching half::f16::to_f32.
 __device__ __forceinline__ float h2f(uint16_t h) {

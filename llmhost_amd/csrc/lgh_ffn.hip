@@ -98,7 +98,7 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
       ss += x2 * x2;
       ss += x3 * x3;
     }
-    for (int off = kWave / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    ss = wave_sum_dpp64(ss);
     if (lane == 0) s_ss[wave] = ss;
     __syncthreads();
     double tot = 0.0;
