@@ -143,22 +143,35 @@ int lgh_q8_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *x, float *y, size_t 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev,
                     size_t tokens);
 
-/* ---- decode FFN block (SwiGLU) ---------------------------------------------
- * Lfm2::ffn_residual_in (crates/llm-engine/src/lfm2.rs:883-911) for one token:
- *   normed = rms_norm(hidden, norm_w, eps)  (crates/llm-cpu/src/ops.rs:8-23;
- *            norm_w == NULL: normed = hidden)
- *   g, u   = W1 normed, W3 normed           (gemv_q4_pair, gemv_q4.rs:396-443)
- *   h      = silu(g) * u                    (ops.rs:27-36, lfm2.rs:902-905)
- *   hidden = (float)((double)hidden + (double)(W2 h))   (gemv_q4_add)
- * W1, W3: [inter, dim]; W2: [dim, inter]; inter % 32 == 0 and dim <= 2048
- * (LGH_ERR_SHAPE otherwise).  Both activation quantizations follow the
- * context's act-quant mode.  Two launches; the second reads h's ActQ8 codes
- * written by the first.  No reference counterpart as one function: it fuses
- * the sequence of reference calls above. */
+/* ---- elementwise ops of the FFN block ----------------------------------------
+ * rms_norm (crates/llm-cpu/src/ops.rs:8-23): out[r] = w * (x[r] * scale_r)
+ * over `rows` rows of `dim`, scale_r = f32(1 / sqrt(sum_sq * (1/dim) + eps))
+ * with the sum of squares in f64.  out may be x. */
+int lgh_rms_norm(lgh_ctx *ctx, const float *x, const float *weight, size_t dim, size_t rows, float eps,
+                 float *out);
+int lgh_rms_norm_dev(lgh_ctx *ctx, const float *x_dev, const float *weight_dev, size_t dim, size_t rows,
+                     float eps, float *out_dev);
+/* silu_inplace + the gate multiply (ops.rs:27-36, crates/llm-engine/src/
+ * lfm2.rs:902-905): g[i] = (g[i] / (1 + exp(-g[i]))) * u[i]. */
+int lgh_silu_mul(lgh_ctx *ctx, float *g, const float *u, size_t n);
+int lgh_silu_mul_dev(lgh_ctx *ctx, float *g_dev, const float *u_dev, size_t n);
+
+/* ---- FFN block (SwiGLU) -------------------------------------------------------
+ * Lfm2::ffn_residual (crates/llm-engine/src/lfm2.rs:861-881) and, for one
+ * token, Lfm2::ffn_residual_in (:883-911), over `tokens` rows of hidden:
+ *   normed = rms_norm(hidden, norm_w, eps)  (norm_w == NULL: normed = hidden)
+ *   g, u   = W1 normed, W3 normed           (apply_pair: gemv_q4_pair / gemm_q4)
+ *   h      = silu(g) * u
+ *   hidden = (float)((double)hidden + (double)(W2 h))   (gemv_q4_add / gemm_q4_add)
+ * W1, W3: [inter, dim]; W2: [dim, inter].  Both activation quantizations
+ * follow the context's act-quant mode.  One token with dim <= 2048 runs two
+ * fused launches (the second reads h's ActQ8 codes written by the first);
+ * otherwise the ops above run one after another on the device.  No single
+ * reference function: it replaces the reference's sequence of calls. */
 int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
-                        const float *norm_w, float eps, float *hidden);
+                        const float *norm_w, float eps, float *hidden, size_t tokens);
 int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
-                            const float *norm_w_dev, float eps, float *hidden_dev);
+                            const float *norm_w_dev, float eps, float *hidden_dev, size_t tokens);
 
 /* ---- test hooks (host pointers, synchronous) -------------------------------
  * ActQ8::quantize / quantize_row / quantize_batch (gemv_q4.rs:33-95,
@@ -170,10 +183,10 @@ int lgh_act_quant(lgh_ctx *ctx, const float *x, size_t m, size_t k, int8_t *qs, 
  * int8, using the GEMV's device unpack + dot instructions; bit-exact target. */
 int lgh_q4_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks,
                       int32_t *out);
-/* The first launch of lgh_q4_ffn_residual alone, for tests: g, u, h =
- * silu(g) * u [inter] in f32, and h's PerBlock ActQ8 codes hq [inter] and
- * scales hs [inter/32] as the second launch consumes them (hq, hs may be
- * NULL).  hidden is not modified. */
+/* The first fused launch of lgh_q4_ffn_residual (one token, dim <= 2048)
+ * alone, for tests: g, u, h = silu(g) * u [inter] in f32, and h's PerBlock
+ * ActQ8 codes hq [inter] and scales hs [inter/32] as the second launch
+ * consumes them (hq, hs may be NULL).  hidden is not modified. */
 int lgh_q4_ffn_gate_up(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const float *norm_w, float eps,
                        const float *hidden, float *g, float *u, float *h, int8_t *hq, float *hs);
 /* Integer Q8_0 x Q8 block dot (crates/llm-engine/src/weights.rs:206-209). */

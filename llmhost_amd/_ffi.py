@@ -66,8 +66,12 @@ SIGNATURES = {
     "lgh_q4_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q8_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q4_mfma_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
-    "lgh_q4_ffn_residual": (_I, [_P, _P, _P, _P, _P, C.c_float, _P]),
-    "lgh_q4_ffn_residual_dev": (_I, [_P, _P, _P, _P, _P, C.c_float, _P]),
+    "lgh_rms_norm": (_I, [_P, _P, _P, _SZ, _SZ, C.c_float, _P]),
+    "lgh_rms_norm_dev": (_I, [_P, _P, _P, _SZ, _SZ, C.c_float, _P]),
+    "lgh_silu_mul": (_I, [_P, _P, _P, _SZ]),
+    "lgh_silu_mul_dev": (_I, [_P, _P, _P, _SZ]),
+    "lgh_q4_ffn_residual": (_I, [_P, _P, _P, _P, _P, C.c_float, _P, _SZ]),
+    "lgh_q4_ffn_residual_dev": (_I, [_P, _P, _P, _P, _P, C.c_float, _P, _SZ]),
     "lgh_q4_ffn_gate_up": (_I, [_P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _P, _P]),
 }
 

@@ -520,7 +520,64 @@ int lgh_q4_gemv_pair(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const flo
   return LGH_OK;
 }
 
-// ---- decode FFN block ---------------------------------------------------
+// ---- elementwise ops and the FFN block -------------------------------------
+int lgh_rms_norm_dev(lgh_ctx *ctx, const float *x_dev, const float *w_dev, size_t dim, size_t rows, float eps,
+                     float *out_dev) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (dim == 0 || rows == 0) return LGH_OK;
+  if (!x_dev || !w_dev || !out_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/weight/out");
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_rms_norm(x_dev, w_dev, dim, rows, eps, out_dev, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_rms_norm(lgh_ctx *ctx, const float *x, const float *w, size_t dim, size_t rows, float eps, float *out) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (dim == 0 || rows == 0) return LGH_OK;
+  if (!x || !w || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/weight/out");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = dim * rows * sizeof(float), wb = dim * sizeof(float);
+  const size_t ox = cv.take(xb), ow = cv.take(wb);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *wd = reinterpret_cast<float *>(st + ow);
+  LGH_HIP(ctx, hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(wd, w, wb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_rms_norm_dev(ctx, xd, wd, dim, rows, eps, xd)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(out, xd, xb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_silu_mul_dev(lgh_ctx *ctx, float *g_dev, const float *u_dev, size_t n) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (n == 0) return LGH_OK;
+  if (!g_dev || !u_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null g/u");
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_silu_mul(g_dev, u_dev, n, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_silu_mul(lgh_ctx *ctx, float *g, const float *u, size_t n) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (n == 0) return LGH_OK;
+  if (!g || !u) return fail(ctx, LGH_ERR_INVALID_ARG, "null g/u");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t b = n * sizeof(float);
+  const size_t og = cv.take(b), ou = cv.take(b);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *gd = reinterpret_cast<float *>(st + og), *ud = reinterpret_cast<float *>(st + ou);
+  LGH_HIP(ctx, hipMemcpyAsync(gd, g, b, hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(ud, u, b, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_silu_mul_dev(ctx, gd, ud, n)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(g, gd, b, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
 static int check_ffn(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2) {
   if (!w1 || !w3) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
   if (w1->k != w3->k || w1->n != w3->n)
@@ -528,21 +585,12 @@ static int check_ffn(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh
   if (w2 && (w2->k != w1->n || w2->n != w1->k))
     return fail(ctx, LGH_ERR_SHAPE, "down must be %zux%zu, got %zux%zu", w1->k, w1->n, w2->n, w2->k);
   if (w1->n % 32 != 0) return fail(ctx, LGH_ERR_SHAPE, "intermediate size %zu is not a multiple of 32", w1->n);
-  if (w1->bpr > lgh::kFfnMaxBpr)
-    return fail(ctx, LGH_ERR_SHAPE, "hidden size %zu exceeds %zu", w1->k, lgh::kFfnMaxBpr * 32);
   return LGH_OK;
 }
 
-int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
-                            const float *norm_w_dev, float eps, float *hidden_dev) {
-  if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
-  if (int r = check_ffn(ctx, w1, w3, w2)) return r;
-  if (w1->k == 0 || w1->n == 0) return LGH_OK;  // no hidden elements, or W2 h = 0 (hidden + 0 is hidden)
-  if (!hidden_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
-  if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
-    return fail(ctx, LGH_ERR_INVALID_ARG, "hidden and norm weight must be 16-byte aligned");
-  if (int r = set_device(ctx)) return r;
+// One token on a fused-shape FFN: two launches.
+static int ffn_fused(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2, const float *norm_w_dev,
+                     float eps, float *hidden_dev) {
   const size_t n = w1->n;
   // PerBlock and a GEMV-sized W2: h leaves the gate/up kernel already
   // quantized.  Otherwise (PerRow needs all of h for its scale, or K beyond
@@ -562,23 +610,51 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
   return LGH_OK;
 }
 
-int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2, const float *norm_w,
-                        float eps, float *hidden) {
+int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
+                            const float *norm_w_dev, float eps, float *hidden_dev, size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
   if (int r = check_ffn(ctx, w1, w3, w2)) return r;
-  if (w1->k == 0 || w1->n == 0) return LGH_OK;
+  if (tokens == 0 || w1->k == 0 || w1->n == 0) return LGH_OK;  // nothing, or W2 h = 0 (hidden + 0 is hidden)
+  if (!hidden_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
+  if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "hidden and norm weight must be 16-byte aligned");
+  if (int r = set_device(ctx)) return r;
+  if (tokens == 1 && lgh::ffn_gate_up_supported(w1)) return ffn_fused(ctx, w1, w3, w2, norm_w_dev, eps, hidden_dev);
+  // Several tokens (or a wide model): the reference's sequence of ops
+  // (lfm2.rs:861-881), each on the device, intermediates in the context.
+  const size_t dim = w1->k, inter = w1->n;
+  Carve cv;
+  const size_t o_n = cv.take(norm_w_dev ? tokens * dim * sizeof(float) : 0);
+  const size_t o_g = cv.take(tokens * inter * sizeof(float)), o_u = cv.take(tokens * inter * sizeof(float));
+  if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, cv.off)) return r;
+  char *f = static_cast<char *>(ctx->ffn);
+  float *normed = norm_w_dev ? reinterpret_cast<float *>(f + o_n) : hidden_dev;
+  float *g = reinterpret_cast<float *>(f + o_g), *u = reinterpret_cast<float *>(f + o_u);
+  if (norm_w_dev) LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, dim, tokens, eps, normed, ctx->stream));
+  if (int r = lgh_q4_gemm_dev(ctx, w1, normed, g, tokens, LGH_ASSIGN)) return r;
+  if (int r = lgh_q4_gemm_dev(ctx, w3, normed, u, tokens, LGH_ASSIGN)) return r;
+  LGH_HIP(ctx, lgh::launch_silu_mul(g, u, tokens * inter, ctx->stream));
+  return lgh_q4_gemm_dev(ctx, w2, g, hidden_dev, tokens, LGH_ADD_F64);
+}
+
+int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2, const float *norm_w,
+                        float eps, float *hidden, size_t tokens) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_ffn(ctx, w1, w3, w2)) return r;
+  if (tokens == 0 || w1->k == 0 || w1->n == 0) return LGH_OK;
   if (!hidden) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
   if (int r = set_device(ctx)) return r;
   Carve cv;
-  const size_t xb = w1->k * sizeof(float);
-  const size_t ox = cv.take(xb), on = cv.take(norm_w ? xb : 0);
+  const size_t xb = tokens * w1->k * sizeof(float), nb = w1->k * sizeof(float);
+  const size_t ox = cv.take(xb), on = cv.take(norm_w ? nb : 0);
   if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
   char *st = static_cast<char *>(ctx->stage);
   float *xd = reinterpret_cast<float *>(st + ox), *nd = norm_w ? reinterpret_cast<float *>(st + on) : nullptr;
   LGH_HIP(ctx, hipMemcpyAsync(xd, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
-  if (norm_w) LGH_HIP(ctx, hipMemcpyAsync(nd, norm_w, xb, hipMemcpyHostToDevice, ctx->stream));
-  if (int r = lgh_q4_ffn_residual_dev(ctx, w1, w3, w2, nd, eps, xd)) return r;
+  if (norm_w) LGH_HIP(ctx, hipMemcpyAsync(nd, norm_w, nb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q4_ffn_residual_dev(ctx, w1, w3, w2, nd, eps, xd, tokens)) return r;
   LGH_HIP(ctx, hipMemcpyAsync(hidden, xd, xb, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return LGH_OK;
@@ -589,6 +665,9 @@ int lgh_q4_ffn_gate_up(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const f
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (int r = check_ffn(ctx, w1, w3, nullptr)) return r;
   if (w1->k == 0 || w1->n == 0) return LGH_OK;
+  if (!lgh::ffn_gate_up_supported(w1))
+    return fail(ctx, LGH_ERR_SHAPE, "the fused gate/up stage needs hidden size <= %zu, got %zu",
+                lgh::kFfnMaxBpr * 32, w1->k);
   if (!hidden || !g || !u || !h) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/g/u/h");
   if (int r = set_device(ctx)) return r;
   const size_t n = w1->n, xb = w1->k * sizeof(float), yb = n * sizeof(float);

@@ -159,6 +159,42 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
   }
 }
 
+// rms_norm over rows of dim (ops.rs:8-23): one workgroup per row, the f64
+// sum of squares as a fixed tree (per-thread strided partials, DPP wave sums,
+// the 4 wave sums in order), then out = w * (x * scale) in f32.
+constexpr int kNormThreads = 256;
+
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *__restrict__ x,
+                                                                const float *__restrict__ w, int dim, float eps,
+                                                                float *__restrict__ out) {
+  __shared__ double s_ss[kNormThreads / kWave];
+  const float *row = x + static_cast<size_t>(blockIdx.x) * dim;
+  float *dst = out + static_cast<size_t>(blockIdx.x) * dim;
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < dim; i += kNormThreads) {
+    const double v = row[i];
+    ss += v * v;
+  }
+  ss = wave_sum_dpp64(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0) s_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / kWave; i++) tot += s_ss[i];
+  const double inv_dim = 1.0 / static_cast<double>(dim);
+  const float scale = static_cast<float>(1.0 / sqrt(tot * inv_dim + static_cast<double>(eps)));
+  for (int i = threadIdx.x; i < dim; i += kNormThreads) dst[i] = w[i] * (row[i] * scale);
+}
+
+// g = silu(g) * u (ops.rs:27-36, lfm2.rs:902-905), elementwise.
+__global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ g, const float *__restrict__ u,
+                                                       size_t n) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float x = g[i];
+  g[i] = (x / (1.0f + expf(-x))) * u[i];
+}
+
 template <int BPL>
 hipError_t launch_gate_up(const FfnUpArgs &a, int wgs, hipStream_t st) {
   hipLaunchKernelGGL(ffn_gate_up_kernel<BPL>, dim3(wgs), dim3(kFfnThreads), 0, st, a);
@@ -183,6 +219,20 @@ hipError_t launch_ffn_gate_up(const lgh_q4 *w1, const lgh_q4 *w3, const float *x
     case 3: return launch_gate_up<3>(a, wgs, st);
     default: return launch_gate_up<4>(a, wgs, st);
   }
+}
+
+hipError_t launch_rms_norm(const float *x, const float *w, size_t dim, size_t rows, float eps, float *out,
+                           hipStream_t st) {
+  if (rows == 0 || dim == 0) return hipSuccess;
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, st, x, w,
+                     static_cast<int>(dim), eps, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(float *g, const float *u, size_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, g, u, n);
+  return hipGetLastError();
 }
 
 }  // namespace lgh

@@ -126,6 +126,11 @@ bool ffn_gate_up_supported(const lgh_q4 *w1);
 hipError_t launch_ffn_gate_up(const lgh_q4 *w1, const lgh_q4 *w3, const float *x, const float *norm_w, float eps,
                               int per_row, int8_t *hq, float *hs, float *hf, float *g, float *u,
                               hipStream_t stream);
+// rms_norm (ops.rs:8-23) over `rows` rows of `dim`, and g = silu(g) * u
+// (ops.rs:27-36, lfm2.rs:902-905); device pointers.
+hipError_t launch_rms_norm(const float *x, const float *w, size_t dim, size_t rows, float eps, float *out,
+                           hipStream_t stream);
+hipError_t launch_silu_mul(float *g, const float *u, size_t n, hipStream_t stream);
 // The same GEMV on activations already quantized per block (ActQ8 PerBlock
 // codes [k] + scales [k/32], device pointers), e.g. by the FFN gate/up kernel.
 hipError_t launch_q4_gemv_codes(const lgh_q4 *w, const int8_t *codes, const float *scales, float *y, int mode,

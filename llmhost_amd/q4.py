@@ -340,24 +340,51 @@ def gemv_q4_pair(w_gate: Q4Matrix, w_up: Q4Matrix, x, out_gate, out_up) -> None:
                                      _np_ptr(out_up)))
 
 
-# ---- decode FFN block --------------------------------------------------------
-def ffn_residual(w1: Q4Matrix, w3: Q4Matrix, w2: Q4Matrix, norm_w, eps: float, hidden) -> None:
-    """Lfm2::ffn_residual_in for one token (crates/llm-engine/src/lfm2.rs:883-911): hidden +=
-    W2 (silu(W1 n) * W3 n) with n = rms_norm(hidden, norm_w, eps) (norm_w None: n = hidden);
-    the down projection is added in f64.  hidden is updated in place (numpy or torch)."""
+# ---- FFN block ---------------------------------------------------------------
+def rms_norm(x, weight, eps: float, out, ctx: Context | None = None) -> None:
+    """rms_norm (crates/llm-cpu/src/ops.rs:8-23) over the rows of x (row length = weight size)."""
+    ctx = ctx or default_context()
+    if _is_torch(x):
+        _shape_assert(x.numel() % weight.numel() == 0 and out.numel() == x.numel(), "rms_norm shapes")
+        ctx.check(lib().lgh_rms_norm_dev(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(weight, "weight"), weight.numel(),
+                                         x.numel() // weight.numel(), float(eps), _dev_ptr(out, "out")))
+        return
+    x, weight, out = _host_f32(x, "x"), _host_f32(weight, "weight"), _host_f32(out, "out")
+    _shape_assert(x.size % weight.size == 0 and out.size == x.size, "rms_norm shapes")
+    ctx.check(lib().lgh_rms_norm(ctx.handle, _np_ptr(x), _np_ptr(weight), weight.size, x.size // weight.size,
+                                 float(eps), _np_ptr(out)))
+
+
+def silu_mul(g, u, ctx: Context | None = None) -> None:
+    """g = silu(g) * u in place (ops.rs:27-36, lfm2.rs:902-905)."""
+    ctx = ctx or default_context()
+    if _is_torch(g):
+        _shape_assert(g.numel() == u.numel(), "g/u lengths differ")
+        ctx.check(lib().lgh_silu_mul_dev(ctx.handle, _dev_ptr(g, "g"), _dev_ptr(u, "u"), g.numel()))
+        return
+    g, u = _host_f32(g, "g"), _host_f32(u, "u")
+    _shape_assert(g.size == u.size, "g/u lengths differ")
+    ctx.check(lib().lgh_silu_mul(ctx.handle, _np_ptr(g), _np_ptr(u), g.size))
+
+
+def ffn_residual(w1: Q4Matrix, w3: Q4Matrix, w2: Q4Matrix, norm_w, eps: float, hidden, tokens: int = 1) -> None:
+    """Lfm2::ffn_residual / ffn_residual_in (crates/llm-engine/src/lfm2.rs:861-911) over `tokens`
+    rows: hidden += W2 (silu(W1 n) * W3 n) with n = rms_norm(hidden, norm_w, eps) (norm_w None:
+    n = hidden); the down projection is added in f64.  hidden is updated in place (numpy or
+    torch)."""
     ctx = w1.ctx
     _shape_assert(w1.k == w3.k == w2.n and w1.n == w3.n == w2.k, "FFN shapes: W1, W3 [inter, dim], W2 [dim, inter]")
     if _is_torch(hidden):
-        _shape_assert(hidden.numel() == w1.k, "hidden length != dim")
+        _shape_assert(hidden.numel() == tokens * w1.k, "hidden length != tokens * dim")
         nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
         ctx.check(lib().lgh_q4_ffn_residual_dev(ctx.handle, w1.handle, w3.handle, w2.handle, nw, float(eps),
-                                                _dev_ptr(hidden, "hidden")))
+                                                _dev_ptr(hidden, "hidden"), tokens))
         return
     hidden = _host_f32(hidden, "hidden")
-    _shape_assert(hidden.size == w1.k, "hidden length != dim")
+    _shape_assert(hidden.size == tokens * w1.k, "hidden length != tokens * dim")
     nw = None if norm_w is None else _np_ptr(_host_f32(norm_w, "norm_w"))
     ctx.check(lib().lgh_q4_ffn_residual(ctx.handle, w1.handle, w3.handle, w2.handle, nw, float(eps),
-                                        _np_ptr(hidden)))
+                                        _np_ptr(hidden), tokens))
 
 
 def ffn_gate_up(w1: Q4Matrix, w3: Q4Matrix, norm_w, eps: float, hidden):

@@ -71,7 +71,7 @@ def lib():
         L.oq_q8_apply.argtypes = [P, sz, sz, P, sz, P, i]
         L.oq_rms_norm.argtypes = [P, P, sz, sz, C.c_float, P]
         L.oq_silu_mul.argtypes = [P, P, sz]
-        L.oq_ffn_residual.argtypes = [P, P, P, P, C.c_float, P, i, i, i]
+        L.oq_ffn_residual.argtypes = [P, P, P, P, C.c_float, P, sz, i, i, i]
         L.oq_thread_range.argtypes = [sz, sz, sz, C.POINTER(sz), C.POINTER(sz)]
         L.oq_cpu_has.argtypes, L.oq_cpu_has.restype = [C.c_char_p], i
         _lib = L
@@ -256,14 +256,14 @@ def silu_mul(g, u):
     return out
 
 
-def ffn_residual(w1: "Q4Matrix", w3: "Q4Matrix", w2: "Q4Matrix", norm_w, eps: float, hidden, per_row=False,
-                 kernel=KERNEL_DETECT, threads=1):
-    """Lfm2::ffn_residual_in (lfm2.rs:883-911) for one token; returns the new hidden."""
+def ffn_residual(w1: "Q4Matrix", w3: "Q4Matrix", w2: "Q4Matrix", norm_w, eps: float, hidden, tokens=1,
+                 per_row=False, kernel=KERNEL_DETECT, threads=1):
+    """Lfm2::ffn_residual / ffn_residual_in (lfm2.rs:861-911); returns the new hidden."""
     out = np.array(hidden, dtype=np.float32, copy=True)
-    assert out.size == w1.k == w3.k == w2.n and w1.n == w3.n == w2.k
+    assert out.size == tokens * w1.k and w1.k == w3.k == w2.n and w1.n == w3.n == w2.k
     nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
     lib().oq_ffn_residual(w1.handle, w3.handle, w2.handle, None if nw is None else _p(nw), eps, _p(out),
-                          int(per_row), kernel, threads)
+                          tokens, int(per_row), kernel, threads)
     return out
 
 

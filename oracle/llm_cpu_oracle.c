@@ -828,18 +828,27 @@ void oq_silu_mul(float *g, const float *u, size_t n) {
 }
 
 void oq_ffn_residual(const oq_q4_matrix *w1, const oq_q4_matrix *w3, const oq_q4_matrix *w2,
-                     const float *norm_w, float eps, float *hidden, int per_row, int kernel, int threads) {
+                     const float *norm_w, float eps, float *hidden, size_t tokens, int per_row, int kernel,
+                     int threads) {
   const size_t dim = w1->k, inter = w1->n;
-  float *normed = malloc(dim * sizeof(float));
-  float *g = malloc(inter * sizeof(float));
-  float *u = malloc(inter * sizeof(float));
+  float *normed = malloc(tokens * dim * sizeof(float));
+  float *g = malloc(tokens * inter * sizeof(float));
+  float *u = malloc(tokens * inter * sizeof(float));
   if (norm_w)
-    oq_rms_norm(hidden, norm_w, dim, 1, eps, normed);
+    oq_rms_norm(hidden, norm_w, dim, tokens, eps, normed);
   else
-    memcpy(normed, hidden, dim * sizeof(float));
-  oq_gemv_q4_pair(w1, w3, normed, g, u, per_row, kernel, threads);
-  oq_silu_mul(g, u, inter);
-  oq_gemv_q4(w2, g, hidden, 1, per_row, kernel, threads);
+    memcpy(normed, hidden, tokens * dim * sizeof(float));
+  if (tokens == 1) {  /* apply_pair (weights.rs:106-123): the pair GEMV for one token */
+    oq_gemv_q4_pair(w1, w3, normed, g, u, per_row, kernel, threads);
+  } else {           /* ... else two separate apply calls */
+    oq_gemm_q4(w1, normed, g, tokens, 0, per_row, kernel, threads);
+    oq_gemm_q4(w3, normed, u, tokens, 0, per_row, kernel, threads);
+  }
+  oq_silu_mul(g, u, tokens * inter);
+  if (tokens == 1)
+    oq_gemv_q4(w2, g, hidden, 1, per_row, kernel, threads);
+  else
+    oq_gemm_q4(w2, g, hidden, tokens, 1, per_row, kernel, threads);
   free(normed);
   free(g);
   free(u);

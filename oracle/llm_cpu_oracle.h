@@ -102,11 +102,13 @@ void oq_q8_apply(const oq_block_q8 *blocks, size_t n, size_t k, const float *x,
 void oq_rms_norm(const float *x, const float *weight, size_t dim, size_t rows, float eps, float *out);
 /* silu_inplace (ops.rs:27-36) on g, then g *= u (lfm2.rs:902-905). */
 void oq_silu_mul(float *g, const float *u, size_t n);
-/* Lfm2::ffn_residual_in (lfm2.rs:883-911) for one token: normed =
- * rms_norm(hidden) (weight == NULL: normed = hidden), g, u = gemv_q4_pair,
- * silu(g)*u, hidden = gemv_q4_add(w2, h). */
+/* Lfm2::ffn_residual (lfm2.rs:861-881) / ffn_residual_in (:883-911) over
+ * `tokens` rows: normed = rms_norm(hidden) (norm_w == NULL: normed = hidden),
+ * g, u = apply_pair (pair GEMV for one token, two GEMMs otherwise), silu(g)*u,
+ * hidden = apply_add(w2, h). */
 void oq_ffn_residual(const oq_q4_matrix *w1, const oq_q4_matrix *w3, const oq_q4_matrix *w2,
-                     const float *norm_w, float eps, float *hidden, int per_row, int kernel, int threads);
+                     const float *norm_w, float eps, float *hidden, size_t tokens, int per_row, int kernel,
+                     int threads);
 
 /* ---- pool (pool.rs:212-241 thread_range / for_ranges) ------------------ */
 void oq_thread_range(size_t tid, size_t nthreads, size_t n, size_t *start, size_t *end);

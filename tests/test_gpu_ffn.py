@@ -112,11 +112,87 @@ def test_ffn_shape_errors(gpu_ctx):
     b = synth.q4_blocks(1, 64, 4096)
     big1 = q4.Q4Matrix.from_blocks(64, 4096, b, gpu_ctx)
     big3 = q4.Q4Matrix.from_blocks(64, 4096, b, gpu_ctx)
-    big2 = q4.Q4Matrix.from_blocks(4096, 64, synth.q4_blocks(2, 4096, 64), gpu_ctx)
-    with pytest.raises(Exception, match="exceeds"):
-        q4.ffn_residual(big1, big3, big2, None, 0.0, np.zeros(4096, np.float32))
+    with pytest.raises(Exception, match="hidden size"):  # the fused stage alone needs dim <= 2048
+        q4.ffn_gate_up(big1, big3, None, 0.0, np.zeros(4096, np.float32))
     w1 = q4.Q4Matrix.from_blocks(64, 96, synth.q4_blocks(3, 64, 96), gpu_ctx)
     w3 = q4.Q4Matrix.from_blocks(32, 96, synth.q4_blocks(4, 32, 96), gpu_ctx)
     w2 = q4.Q4Matrix.from_blocks(96, 64, synth.q4_blocks(5, 96, 64), gpu_ctx)
     with pytest.raises(Exception):
         q4.ffn_residual(w1, w3, w2, None, 0.0, np.zeros(96, np.float32))
+
+
+# ---- the elementwise ops and the multi-token block ----------------------------------------
+@pytest.mark.parametrize("dim,rows", [(32, 1), (1536, 1), (1536, 7), (4096, 3), (100 * 32, 2)])
+def test_rms_norm_bit_exact(gpu_ctx, oracle, dim, rows):
+    x = (synth.activations(dim + rows, rows, dim) * np.float32(4.0)).astype(np.float32)
+    w = (1 + 0.3 * synth.normal_f32(dim, dim)).astype(np.float32)
+    got = np.zeros_like(x)
+    q4.rms_norm(x, w, 1e-5, got, gpu_ctx)
+    assert got.tobytes() == oracle.rms_norm(x, w, 1e-5).tobytes()
+
+
+def test_silu_mul_within_exp_ulp(gpu_ctx, oracle):
+    g = np.concatenate([np.linspace(-40, 40, 20001), synth.normal_f32(3, 4096) * 4]).astype(np.float32)
+    u = synth.normal_f32(4, g.size)
+    got = g.copy()
+    q4.silu_mul(got, u, gpu_ctx)
+    # libm's expf and the device's expf each err by up to an ulp, so exp's two values may be two
+    # ulp apart; through 1 + exp, the divide and the multiply the results stay within 4 ulp.
+    ref = oracle.silu_mul(g, u).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - ref) / (ulp + 1e-45)
+    assert err.max() <= 4, (err.max(), g[np.argmax(err)])
+    assert np.mean(got == ref.astype(np.float32)) > 0.9
+
+
+def _per_op(gpu_mats, nw, hidden, t):
+    """The block composed from the library's per-op entry points (the multi-token path's own
+    sequence of launches)."""
+    g1, g3, g2 = gpu_mats
+    normed = np.zeros_like(hidden)
+    if nw is not None:
+        q4.rms_norm(hidden, nw, 1e-5, normed, g1.ctx)
+    else:
+        normed = hidden.copy()
+    g = np.zeros(t * g1.n, np.float32)
+    u = np.zeros(t * g1.n, np.float32)
+    if t == 1:
+        q4.gemv_q4_pair(g1, g3, normed, g, u)
+    else:
+        q4.gemm_q4(g1, normed, g, t)
+        q4.gemm_q4(g3, normed, u, t)
+    q4.silu_mul(g, u, g1.ctx)
+    out = hidden.copy()
+    (q4.gemv_q4_add(g2, g, out) if t == 1 else q4.gemm_q4_add(g2, g, out, t))
+    return out
+
+
+@pytest.mark.parametrize("dim,inter,t", [(1536, 8192, 1), (1536, 8192, 4), (1536, 8192, 16), (96, 64, 70),
+                                         (4096, 64, 1), (544, 160, 3)])
+def test_ffn_residual_matches_per_op_composition(gpu_ctx, oracle, dim, inter, t):
+    """Every path of lgh_q4_ffn_residual equals the per-op composition bit for bit (the fused
+    one-token launches included: same dots, same silu, same codes), and the oracle's
+    composition up to the ties one ulp of exp can move."""
+    gpu, cpu = _mats(gpu_ctx, oracle, dim, inter, 90 + t + dim)
+    hidden = (synth.activations(100 + t, t, dim) * np.float32(2.0)).astype(np.float32).ravel()
+    nw = (1 + 0.2 * synth.normal_f32(101, dim)).astype(np.float32)
+    got = hidden.copy()
+    q4.ffn_residual(*gpu, nw, 1e-5, got, tokens=t)
+    assert got.tobytes() == _per_op(gpu, nw, hidden, t).tobytes()
+    ref = oracle.ffn_residual(*cpu, nw, 1e-5, hidden, tokens=t, threads=8)
+    assert_close(got, ref, atol=2e-2, rtol=1e-3, what="vs reference composition")
+
+
+def test_ffn_residual_tokens_device_path(gpu_ctx, oracle):
+    import torch
+
+    dim, inter, t = 1536, 8192, 8
+    gpu, _ = _mats(gpu_ctx, oracle, dim, inter, 120)
+    hidden = synth.activations(121, t, dim).ravel()
+    nw = (1 + 0.2 * synth.normal_f32(122, dim)).astype(np.float32)
+    host = hidden.copy()
+    q4.ffn_residual(*gpu, nw, 1e-5, host, tokens=t)
+    dev = torch.from_numpy(hidden.copy()).cuda()
+    q4.ffn_residual(*gpu, torch.from_numpy(nw).cuda(), 1e-5, dev, tokens=t)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev.cpu().numpy(), host)

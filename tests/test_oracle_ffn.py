@@ -78,3 +78,21 @@ def test_ffn_residual_is_the_reference_composition(oracle):
     g, u = oracle.gemv_q4_pair(w1, w3, hidden)
     ref = oracle.gemv_q4(w2, oracle.silu_mul(g, u), out=hidden.copy(), add=True)
     assert got.tobytes() == ref.tobytes()
+
+
+def test_ffn_residual_tokens_is_the_reference_composition(oracle):
+    """Lfm2::ffn_residual (lfm2.rs:861-881): rms_norm per row, two GEMMs (apply_pair with
+    tokens > 1), silu * u, gemm_q4_add."""
+    dim, inter, t = 64, 96, 5
+    w1 = oracle.Q4Matrix(inter, dim, synth.q4_blocks(11, inter, dim))
+    w3 = oracle.Q4Matrix(inter, dim, synth.q4_blocks(12, inter, dim))
+    w2 = oracle.Q4Matrix(dim, inter, synth.q4_blocks(13, dim, inter))
+    hidden = synth.activations(14, t, dim)
+    nw = (1 + 0.1 * synth.normal_f32(15, dim)).astype(np.float32)
+    got = oracle.ffn_residual(w1, w3, w2, nw, 1e-5, hidden, tokens=t)
+    normed = oracle.rms_norm(hidden, nw, 1e-5)
+    g = oracle.gemm_q4(w1, normed, t)
+    u = oracle.gemm_q4(w3, normed, t)
+    h = oracle.silu_mul(g, u)
+    ref = oracle.gemm_q4(w2, h, t, out=hidden.copy(), add=True)
+    assert got.tobytes() == ref.tobytes()
