@@ -189,25 +189,33 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---- exact fast divisions for ActQ8 -----------------------------------------
-// RN(a / 127) for every finite a >= 0: q0 = a*y with y = RN(1/127), then one
-// Markstein correction q = fma(fma(-q0, 127, a), y, q0).  Proven exhaustively
-// over all 2^31 non-negative floats (denormals included) by
-// tests/fastquant_check.c.
+// RN(a / 127) for every a >= 0: q0 = a*y with y = RN(1/127), then one
+// Markstein correction q = fma(fma(-q0, 127, a), y, q0), proven exhaustively
+// over every finite a >= 0 (denormals included) by tests/fastquant_check.c.
+// At a = +inf the correction term is inf - inf, so inf / 127 = inf is
+// selected directly.
 __device__ __forceinline__ float div127_rn(float a) {
   const float y = 0x1.020408p-7f;  // RN(1/127)
   const float q0 = a * y;
-  return fmaf(fmaf(-q0, 127.0f, a), y, q0);
+  const float q = fmaf(fmaf(-q0, 127.0f, a), y, q0);
+  return a == __builtin_inff() ? a : q;
 }
 
 // RN(1 / s) for s > 0: v_rcp_f32 (faithful, 1 ulp) refined by one FMA Newton
 // step, which tests/fastquant_check.c proves correctly rounded for either
 // faithful starting value for every s in [2^-126, 2^126) except the
-// all-ones significand; those and out-of-range s use the IEEE division.
+// all-ones significand; those and out-of-range s use the IEEE division, on a
+// real branch: the division's operand passes through an empty asm inside it,
+// so the compiler cannot compute the division for every lane and select.
 __device__ __forceinline__ float recip_rn(float s) {
   const float y0 = __builtin_amdgcn_rcpf(s);
   float q = fmaf(fmaf(-s, y0, 1.0f), y0, y0);
   const uint32_t b = __builtin_bit_cast(uint32_t, s);
-  if (b < 0x00800000u || b >= 0x7E800000u || (b & 0x7FFFFFu) == 0x7FFFFFu) q = __fdiv_rn(1.0f, s);
+  if (b < 0x00800000u || b >= 0x7E800000u || (b & 0x7FFFFFu) == 0x7FFFFFu) {
+    float t = s;
+    asm volatile("" : "+v"(t));
+    q = __fdiv_rn(1.0f, t);
+  }
   return q;
 }
 
@@ -241,11 +249,16 @@ __device__ __forceinline__ int quant_code_ref(float v, float inv) {
 // With per_row, `row_scale` (= row amax / 127) replaces the block scale.
 __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float row_scale, float &scale,
                                                 int &sum) {
-  // 8-lane max/sum by DPP: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror.
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, dpp<0xB1>(amax));
-  amax = fmaxf(amax, dpp<0x4E>(amax));
-  amax = fmaxf(amax, dpp<0x141>(amax));
+  // amax folds |v| into 0.0 with Rust's f32::max, which skips NaN: each
+  // lane's partial starts at 0 and is never NaN, and non-negative floats
+  // order like their bit patterns, so the 8-lane max (DPP quad_perm
+  // [1,0,3,2], [2,3,0,1], row_half_mirror) runs on integers.
+  const float m4 = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.0f);
+  uint32_t mb = __builtin_bit_cast(uint32_t, m4);
+  mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0xB1, 0xf, 0xf, false)));
+  mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x4E, 0xf, 0xf, false)));
+  mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x141, 0xf, 0xf, false)));
+  const float amax = __builtin_bit_cast(float, mb);
   scale = per_row ? row_scale : div127_rn(amax);
   const float inv = scale == 0.0f ? 0.0f : recip_rn(scale);
   const float inv2 = 2.0f * inv;
@@ -266,7 +279,8 @@ __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float ro
   s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xf, 0xf, false);
   s += __builtin_amdgcn_update_dpp(0, s, 0x141, 0xf, 0xf, false);
   sum = s;
-  return (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (static_cast<int>(static_cast<uint32_t>(q3) << 24));
+  // low bytes of q0..q3 -> bytes 0..3 (selector 0x0c reads as zero)
+  return static_cast<int>(__builtin_amdgcn_perm(q1, q0, 0x0c0c0400u) | __builtin_amdgcn_perm(q3, q2, 0x04000c0cu));
 }
 
 // ---- x -> LDS codes, shared by the GEMV-style kernels --------------------

@@ -45,6 +45,45 @@ def test_act_quant_ties(gpu_ctx, oracle):
     assert act.scales[0, 0] == 1.0 and act.scales[0, 1] == 0.0
 
 
+def _nan_blocks(k, seed):
+    """x with NaN edge blocks: Rust's amax folds |v| into 0.0 with f32::max, which skips NaN,
+    so an all-NaN block has scale 0, and `NaN as i8` is 0."""
+    x = synth.normal_f32(seed, k) * np.float32(3.0)
+    x[:32] = np.nan                       # all NaN: amax 0, scale 0, codes 0
+    x[32:64:3] = np.nan                   # some NaN: the others set amax
+    x[96:128] = 0.0
+    x[100] = np.float32(1e-40)            # denormal amax: 1/scale overflows
+    x[128:160:5] = -np.inf                # inf amax: scale inf, inv 0, codes NaN -> 0
+    return _f32(x)
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_act_quant_nan_and_inf_blocks(gpu_ctx, oracle, per_row):
+    x = np.stack([_nan_blocks(256, 7), _nan_blocks(256, 6)[::-1].copy()])
+    x[1, 128:160] = 0.25  # the second row finite apart from NaN
+    act = (q4.ActQ8.quantize_row if per_row else q4.ActQ8.quantize)(_f32(x), gpu_ctx)
+    qs, sc, su = oracle.act_quantize(_f32(x), per_row)
+    assert np.array_equal(act.scales.view(np.uint32), sc.view(np.uint32))
+    assert np.array_equal(act.qs, qs)
+    assert np.array_equal(act.sums, su)
+    if not per_row:
+        assert act.scales[0, 0] == 0.0 and not act.qs[0, :32].any()
+        assert act.scales[0, 4] == np.inf  # inf / 127
+
+
+def test_gemv_nan_blocks_match_oracle(gpu_ctx, oracle):
+    """The GEMV's in-kernel quantizer on NaN blocks (no inf: 0 * inf would make the row NaN)."""
+    n, k = 96, 1536
+    x = _nan_blocks(k, 8)
+    x[128:160] = 0.5
+    b = synth.q4_blocks(9, n, k)
+    y = np.zeros(n, np.float32)
+    q4.gemv_q4(q4.Q4Matrix.from_blocks(n, k, b, gpu_ctx), x, y)
+    ref = oracle.gemv_q4(oracle.Q4Matrix(n, k, b), x)
+    assert np.isfinite(ref).all()
+    assert_close(y, ref)
+
+
 def _pattern_block(seed):
     i = np.arange(32)
     w = (((i * 17 + seed) % 21) - 10).astype(np.float32) * np.float32(0.25)
