@@ -127,6 +127,22 @@ int lgh_q4_gemv_pair(lgh_ctx *ctx, const lgh_q4 *w_gate, const lgh_q4 *w_up, con
 int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *w_gate, const lgh_q4 *w_up,
                          const float *x_dev, float *yg_dev, float *yu_dev);
 
+/* gemv_q4_prep / gemv_q4_prep_add (crates/llm-cpu/src/gemv_q4.rs:366-393): the
+ * GEMV on activations already quantized by ActQ8 -- codes int8[k] and block
+ * scales f32[k/32] as lgh_act_quant(_dev) writes them, in either act-quant
+ * mode (the sums are not read).  The reference's Q4Kernel argument has no
+ * counterpart (one device kernel).  K <= 32768.  Device codes 16-byte and
+ * scales 4-byte aligned. */
+int lgh_q4_gemv_prep(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, const float *scales, float *y, int mode);
+int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, const float *scales_dev,
+                         float *y_dev, int mode);
+/* ActQ8::quantize_into / quantize_row_into (gemv_q4.rs:52-95) per row of
+ * x[m,k], device to device, enqueued on the context stream and honouring the
+ * context's act-quant mode: codes[m,k], scales[m,k/32], sums[m,k/32] (sums may
+ * be NULL).  x 16-byte aligned, the outputs 4-byte aligned. */
+int lgh_act_quant_dev(lgh_ctx *ctx, const float *x_dev, size_t m, size_t k, int8_t *qs_dev, float *scales_dev,
+                      int32_t *sums_dev);
+
 /* ---- Q4 GEMM, M >= 1 ------------------------------------------------------
  * gemm_q4 / gemm_q4_add (crates/llm-cpu/src/gemv_q4.rs:686-722):
  * y[m, n] = x[m, k] @ W[n, k]^T, activations quantized per token with

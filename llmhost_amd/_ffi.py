@@ -63,6 +63,9 @@ SIGNATURES = {
     "lgh_q8_gemv": (_I, [_P, _P, _P, _P, _SZ]),
     "lgh_q8_gemv_dev": (_I, [_P, _P, _P, _P, _SZ]),
     "lgh_act_quant": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),
+    "lgh_act_quant_dev": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),
+    "lgh_q4_gemv_prep": (_I, [_P, _P, _P, _P, _P, _I]),
+    "lgh_q4_gemv_prep_dev": (_I, [_P, _P, _P, _P, _P, _I]),
     "lgh_q4_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q8_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q4_mfma_block_dots": (_I, [_P, _P, _P, _SZ, _P]),

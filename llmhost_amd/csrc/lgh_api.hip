@@ -401,6 +401,70 @@ int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const
   return launch_gemv(ctx, wg, yg_dev, wu, yu_dev, x_dev, LGH_ASSIGN);
 }
 
+// gemv_q4_prep / gemv_q4_prep_add: the GEMV kernel reads ActQ8 codes and
+// block scales (either act-quant mode) instead of loading and quantizing x.
+int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, const float *scales_dev,
+                         float *y_dev, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && (!qs_dev || !scales_dev))) return fail(ctx, LGH_ERR_INVALID_ARG, "null codes/scales/y");
+  if (!aligned16(qs_dev) || (reinterpret_cast<uintptr_t>(scales_dev) & 3u))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "codes must be 16-byte and scales 4-byte aligned");
+  if (!lgh::plan_q4_gemv(w->n, w->bpr, 1).ok)
+    return fail(ctx, LGH_ERR_SHAPE, "K=%zu: the prepared-activation GEMV supports K <= 32768", w->k);
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_q4_gemv_codes(w, qs_dev, scales_dev, y_dev, mode, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_gemv_prep(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, const float *scales, float *y, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (w->n == 0) return LGH_OK;
+  if (!y || (w->k && (!qs || !scales))) return fail(ctx, LGH_ERR_INVALID_ARG, "null codes/scales/y");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t qb = w->k, sb = w->bpr * sizeof(float), yb = w->n * sizeof(float);
+  const size_t oq = cv.take(qb), os = cv.take(sb), oy = cv.take(yb);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  auto *qd = reinterpret_cast<int8_t *>(st + oq);
+  auto *sd = reinterpret_cast<float *>(st + os);
+  auto *yd = reinterpret_cast<float *>(st + oy);
+  if (qb) LGH_HIP(ctx, hipMemcpyAsync(qd, qs, qb, hipMemcpyHostToDevice, ctx->stream));
+  if (sb) LGH_HIP(ctx, hipMemcpyAsync(sd, scales, sb, hipMemcpyHostToDevice, ctx->stream));
+  if (mode == LGH_ADD_F64) LGH_HIP(ctx, hipMemcpyAsync(yd, y, yb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q4_gemv_prep_dev(ctx, w, qd, sd, yd, mode)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+// ActQ8::quantize_into / quantize_row_into over m rows, device to device; the
+// PerRow row scales go through the GEMM workspace.
+int lgh_act_quant_dev(lgh_ctx *ctx, const float *x_dev, size_t m, size_t k, int8_t *qs_dev, float *scales_dev,
+                      int32_t *sums_dev) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (k % 32) return fail(ctx, LGH_ERR_SHAPE, "activation length %zu is not a multiple of 32", k);
+  if (m == 0 || k == 0) return LGH_OK;
+  if (!x_dev || !qs_dev || !scales_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (!aligned16(x_dev) || (reinterpret_cast<uintptr_t>(qs_dev) & 3u) ||
+      (reinterpret_cast<uintptr_t>(scales_dev) & 3u) || (reinterpret_cast<uintptr_t>(sums_dev) & 3u))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte and codes, scales, sums 4-byte aligned");
+  if (int r = set_device(ctx)) return r;
+  float *row_scale = nullptr;
+  if (ctx->act_mode == LGH_ACT_PER_ROW) {
+    if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, m * sizeof(float))) return r;
+    row_scale = static_cast<float *>(ctx->ws);
+  }
+  LGH_HIP(ctx, lgh::launch_act_quant(x_dev, m, k, ctx->act_mode, qs_dev, scales_dev, sums_dev, row_scale,
+                                     ctx->stream));
+  return LGH_OK;
+}
+
 int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");

@@ -29,7 +29,7 @@ import threading
 import numpy as np
 
 from . import _ffi
-from ._ffi import LghShapeError, check, lib
+from ._ffi import LghError, LghShapeError, check, lib
 from .formats import BLOCK_Q4, BLOCK_Q8_0, BLOCK_SIZE
 
 
@@ -120,6 +120,13 @@ def _dev_ptr(a, name: str) -> C.c_void_p:
 
     if a.device.type != "cuda" or a.dtype != torch.float32 or not a.is_contiguous():
         raise TypeError(f"{name} must be a contiguous float32 tensor on the GPU")
+    return C.c_void_p(a.data_ptr())
+
+
+def _dev_ptr_of(a, name: str, dtype) -> C.c_void_p:
+    """Device pointer of a contiguous tensor of `dtype` on the GPU."""
+    if a.device.type != "cuda" or a.dtype != dtype or not a.is_contiguous():
+        raise TypeError(f"{name} must be a contiguous {dtype} tensor on the GPU")
     return C.c_void_p(a.data_ptr())
 
 
@@ -257,8 +264,10 @@ class ActQ8:
         self.sums = sums
 
     @classmethod
-    def _run(cls, x: np.ndarray, mode: ActQuant, ctx: Context | None) -> "ActQ8":
+    def _run(cls, x, mode: ActQuant, ctx: Context | None) -> "ActQ8":
         ctx = ctx or default_context()
+        if _is_torch(x):
+            return cls._run_dev(x, mode, ctx)
         x = _host_f32(np.ascontiguousarray(x, dtype=np.float32), "x")
         k = x.shape[-1]
         _shape_assert(k % BLOCK_SIZE == 0, f"activation length {k} is not a multiple of {BLOCK_SIZE}")
@@ -270,6 +279,27 @@ class ActQ8:
         ctx.set_act_quant(mode)
         try:
             ctx.check(lib().lgh_act_quant(ctx.handle, _np_ptr(x), m, k, _np_ptr(qs), _np_ptr(sc), _np_ptr(su)))
+        finally:
+            ctx.set_act_quant(prev)
+        return cls(qs, sc, su)
+
+    @classmethod
+    def _run_dev(cls, x, mode: ActQuant, ctx: Context) -> "ActQ8":
+        """Device tensors in and out, enqueued on the context stream (lgh_act_quant_dev)."""
+        import torch
+
+        k = x.shape[-1]
+        _shape_assert(k % BLOCK_SIZE == 0, f"activation length {k} is not a multiple of {BLOCK_SIZE}")
+        m = x.numel() // k if k else 0
+        qs = torch.zeros(x.shape, dtype=torch.int8, device=x.device)
+        sc = torch.zeros(x.shape[:-1] + (k // 32,), dtype=torch.float32, device=x.device)
+        su = torch.zeros(x.shape[:-1] + (k // 32,), dtype=torch.int32, device=x.device)
+        prev = ctx.act_quant()
+        ctx.set_act_quant(mode)
+        try:
+            ctx.check(lib().lgh_act_quant_dev(ctx.handle, _dev_ptr(x, "x"), m, k, _dev_ptr_of(qs, "qs", torch.int8),
+                                              _dev_ptr_of(sc, "scales", torch.float32),
+                                              _dev_ptr_of(su, "sums", torch.int32)))
         finally:
             ctx.set_act_quant(prev)
         return cls(qs, sc, su)
@@ -308,6 +338,37 @@ def gemv_q4(w: Q4Matrix, x, out) -> None:
 def gemv_q4_add(w: Q4Matrix, x, dst) -> None:
     """Adds the product onto dst in f64 (gemv_q4.rs:355-363)."""
     _gemm(w, x, dst, 1, _ffi.LGH_ADD_F64)
+
+
+def _gemv_prep(w: Q4Matrix, acts: ActQ8, out, mode: int) -> None:
+    ctx = w.ctx
+    if _is_torch(acts.qs) or _is_torch(out):
+        import torch
+
+        _shape_assert(acts.qs.numel() == w.k, f"acts length {acts.qs.numel()} != {w.k}")
+        _shape_assert(acts.scales.numel() == w.k // 32, f"acts scales {acts.scales.numel()} != {w.k // 32}")
+        _shape_assert(out.numel() == w.n, f"out length {out.numel()} != {w.n}")
+        ctx.check(lib().lgh_q4_gemv_prep_dev(ctx.handle, w.handle, _dev_ptr_of(acts.qs, "acts.qs", torch.int8),
+                                             _dev_ptr_of(acts.scales, "acts.scales", torch.float32),
+                                             _dev_ptr(out, "out"), mode))
+        return
+    qs = np.ascontiguousarray(acts.qs, dtype=np.int8)
+    sc = _host_f32(np.ascontiguousarray(acts.scales, dtype=np.float32), "acts.scales")
+    out = _host_f32(out, "out")
+    _shape_assert(qs.size == w.k, f"acts length {qs.size} != {w.k}")
+    _shape_assert(sc.size == w.k // 32, f"acts scales {sc.size} != {w.k // 32}")
+    _shape_assert(out.size == w.n, f"out length {out.size} != {w.n}")
+    ctx.check(lib().lgh_q4_gemv_prep(ctx.handle, w.handle, _np_ptr(qs), _np_ptr(sc), _np_ptr(out), mode))
+
+
+def gemv_q4_prep(w: Q4Matrix, acts: ActQ8, out) -> None:
+    """GEMV on already-quantized activations (gemv_q4.rs:366-378)."""
+    _gemv_prep(w, acts, out, _ffi.LGH_ASSIGN)
+
+
+def gemv_q4_prep_add(w: Q4Matrix, acts: ActQ8, dst) -> None:
+    """Fused add variant of gemv_q4_prep (gemv_q4.rs:380-393)."""
+    _gemv_prep(w, acts, dst, _ffi.LGH_ADD_F64)
 
 
 def gemm_q4(w: Q4Matrix, x, out, m: int) -> None:

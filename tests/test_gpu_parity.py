@@ -84,6 +84,78 @@ def test_gemv_nan_blocks_match_oracle(gpu_ctx, oracle):
     assert_close(y, ref)
 
 
+# ---- gemv_q4_prep and the device act-quant ---------------------------------------------
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("n,k", [(8192, 1536), (1536, 8192), (70, 96), (33, 32 * 33), (5, 32768)])
+def test_gemv_prep_matches_oracle(gpu_ctx, oracle, n, k, per_row):
+    """gemv_q4_prep / _add (gemv_q4.rs:366-393) on the device's ActQ8 of x (bit-exact to the
+    oracle's), against the oracle's gemv_q4_prep on the same codes."""
+    b = synth.q4_blocks(40 + n + k, n, k)
+    wg, wc = q4.Q4Matrix.from_blocks(n, k, b, gpu_ctx), oracle.Q4Matrix(n, k, b)
+    x = synth.normal_f32(41 + k, k)
+    acts = (q4.ActQ8.quantize_row if per_row else q4.ActQ8.quantize)(x.reshape(1, -1), gpu_ctx)
+    qs, sc, _ = oracle.act_quantize(x.reshape(1, -1), per_row)
+    assert np.array_equal(acts.qs, qs) and np.array_equal(acts.scales.view(np.uint32), sc.view(np.uint32))
+    got = np.zeros(n, np.float32)
+    q4.gemv_q4_prep(wg, acts, got)
+    assert_close(got, oracle.gemv_q4_prep(wc, qs, sc, threads=8), what="prep")
+    base = synth.normal_f32(42, n)
+    got = base.copy()
+    q4.gemv_q4_prep_add(wg, acts, got)
+    assert_close(got, oracle.gemv_q4_prep(wc, qs, sc, out=base.copy(), add=True, threads=8), what="prep_add")
+    wg.free()
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_device_act_quant_and_prep_equal_the_gemv(gpu_ctx, per_row):
+    """lgh_act_quant_dev equals the host hook bit for bit, and the prepared-activation GEMV on
+    its codes equals the GEMV that quantizes x itself, bit for bit (same codes, same kernel)."""
+    import torch
+
+    n, k, m = 1536, 8192, 3
+    x = synth.activations(43, m, k)
+    mode = q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock
+    host = (q4.ActQ8.quantize_row if per_row else q4.ActQ8.quantize)(x, gpu_ctx)
+    dev = (q4.ActQ8.quantize_row if per_row else q4.ActQ8.quantize)(torch.from_numpy(x).cuda(), gpu_ctx)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev.qs.cpu().numpy(), host.qs)
+    assert np.array_equal(dev.scales.cpu().numpy().view(np.uint32), host.scales.view(np.uint32))
+    assert np.array_equal(dev.sums.cpu().numpy(), host.sums)
+    w = q4.Q4Matrix.from_blocks(n, k, synth.q4_blocks(44, n, k), gpu_ctx)
+    y_prep = torch.zeros(n, device="cuda")
+    y_gemv = torch.zeros(n, device="cuda")
+    row = q4.ActQ8(dev.qs[1].contiguous(), dev.scales[1].contiguous(), dev.sums[1].contiguous())
+    q4.gemv_q4_prep(w, row, y_prep)
+    gpu_ctx.set_act_quant(mode)
+    try:
+        q4.gemv_q4(w, torch.from_numpy(x[1].copy()).cuda(), y_gemv)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    torch.cuda.synchronize()
+    assert torch.equal(y_prep, y_gemv)
+    w.free()
+
+
+def test_gemv_prep_errors(gpu_ctx):
+    import torch
+
+    w = q4.Q4Matrix.from_blocks(64, 96, synth.q4_blocks(45, 64, 96), gpu_ctx)
+    acts = q4.ActQ8.quantize(synth.normal_f32(46, 96).reshape(1, -1), gpu_ctx)
+    with pytest.raises(q4.LghShapeError):
+        q4.gemv_q4_prep(w, q4.ActQ8(acts.qs[:, :64], acts.scales[:, :2], acts.sums), np.zeros(64, np.float32))
+    qd = torch.zeros(97, dtype=torch.int8, device="cuda")
+    sd = torch.zeros(3, dtype=torch.float32, device="cuda")
+    y = torch.zeros(64, device="cuda")
+    with pytest.raises(q4.LghError, match="aligned"):  # codes one byte past a 16-byte boundary
+        q4.gemv_q4_prep(w, q4.ActQ8(qd[1:], sd, None), y)
+    big = q4.Q4Matrix.from_blocks(4, 32 * 1025, synth.q4_blocks(47, 4, 32 * 1025), gpu_ctx)
+    with pytest.raises(q4.LghShapeError, match="32768"):
+        q4.gemv_q4_prep(big, q4.ActQ8(np.zeros(32 * 1025, np.int8), np.zeros(1025, np.float32), None),
+                        np.zeros(4, np.float32))
+    w.free()
+    big.free()
+
+
 def _pattern_block(seed):
     i = np.arange(32)
     w = (((i * 17 + seed) % 21) - 10).astype(np.float32) * np.float32(0.25)
