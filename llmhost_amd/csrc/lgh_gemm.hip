@@ -35,7 +35,7 @@ constexpr int kThreads = 256;
 constexpr int kWRec = static_cast<int>(kMxWRec);
 constexpr int kARec = static_cast<int>(kMxARec);
 constexpr int kTile = static_cast<int>(kMxTile);
-constexpr long kSplitTarget = 256;  // workgroups worth filling the chip with (one per CU)
+constexpr long kSplitTarget = 512;  // two workgroups per CU (M=512, K=10752, N=2048: 61.5 -> 48.6 us vs one)
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]

@@ -242,43 +242,45 @@ __device__ __forceinline__ void store_hl_group8(uint8_t *rec, int s, int tok, ui
   }
 }
 
-// Activations: one 8-lane group per (token, block) over the padded ranges
-// [0, 32*mt) x [0, 2*pp), blocks fastest so x is read contiguously.  Each
-// group handles kActJobs of them, `stride` groups apart, with every x load
-// issued before the first is used.  The h / l E3M2 codes of each int8 code
-// come from a 256-entry LDS table built per workgroup (q + 128 ->
-// code(h) | code(l) << 6), a lookup in place of ~25 VALU per code.
+// Activations: a workgroup builds kActJobs half-records, each the h and l
+// code tiles of one block for one 32-token tile (1536 contiguous bytes) plus
+// its 32 scales.  8-lane group i quantizes token 32 T + i of the block; the
+// tiles are assembled in LDS and written with 16-byte stores, so every line
+// of the image is written whole by one workgroup.  The h / l E3M2 codes of
+// each int8 code come from a 256-entry LDS table built per workgroup
+// (q + 128 -> code(h) | code(l) << 6), a lookup in place of ~25 VALU per code.
 constexpr int kActJobs = 2;
 
 __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, int m, int bpr,
                                                                 int pp, int per_row,
-                                                                const float *row_scale, uint32_t groups,
-                                                                uint32_t stride, uint8_t *mxa) {
+                                                                const float *row_scale, uint32_t units,
+                                                                uint8_t *mxa) {
   __shared__ uint16_t s_hl[256];
-  static_assert(kThreads == 256, "one table entry per thread");
+  __shared__ __align__(16) uint8_t s_tile[kActJobs][2 * kMxTile];
+  __shared__ float s_scale[kActJobs][32];
+  static_assert(kThreads == 256, "one table entry per thread, 32 groups = 32 tokens");
   {
     int h, l;
     split_h_l(static_cast<int>(threadIdx.x) - 128, h, l);
     s_hl[threadIdx.x] = static_cast<uint16_t>(e3m2_code(h) | (e3m2_code(l) << 6));
   }
-  const uint32_t g0 = (blockIdx.x * kThreads + threadIdx.x) >> 3;
-  const int g = threadIdx.x & 7;
+  const int i = threadIdx.x >> 3, g = threadIdx.x & 7, r = g & 3;
   const uint32_t bp2 = 2u * static_cast<uint32_t>(pp);
   float4 v[kActJobs];
 #pragma unroll
   for (int j = 0; j < kActJobs; j++) {
-    const uint32_t gi = g0 + j * stride;
-    const int t = static_cast<int>(gi / bp2), b = static_cast<int>(gi % bp2);
+    const uint32_t u = blockIdx.x * kActJobs + j;  // half-record: token tile u / bp2, block u % bp2
+    const int t = static_cast<int>(u / bp2) * 32 + i, b = static_cast<int>(u % bp2);
     v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (gi < groups && t < m && b < bpr) v[j] = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
+    if (u < units && t < m && b < bpr)
+      v[j] = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
   }
-  __syncthreads();
+  __syncthreads();  // the table
 #pragma unroll
   for (int j = 0; j < kActJobs; j++) {
-    const uint32_t gi = g0 + j * stride;
-    if (gi >= groups) break;  // uniform across each 8-lane group
-    const int t = static_cast<int>(gi / bp2), b = static_cast<int>(gi % bp2);
-    const bool ok = t < m && b < bpr;
+    const uint32_t u = blockIdx.x * kActJobs + j;
+    const int t = static_cast<int>(u / bp2) * 32 + i, b = static_cast<int>(u % bp2);
+    const bool ok = u < units && t < m && b < bpr;
     const bool pr = ok && per_row;
     const float rs = pr ? row_scale[t] : 0.0f;
     float scale;
@@ -286,14 +288,31 @@ __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__r
     const int q = act_quant_group8(v[j], pr, rs, scale, sum);
     uint32_t vh = 0, vl = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t hl = s_hl[(q >> (8 * i)) + 128 & 255];
-      vh |= (hl & 63u) << (6 * i);
-      vl |= (hl >> 6) << (6 * i);
+    for (int e = 0; e < 4; e++) {
+      const uint32_t hl = s_hl[(q >> (8 * e)) + 128 & 255];
+      vh |= (hl & 63u) << (6 * e);
+      vl |= (hl >> 6) << (6 * e);
     }
-    uint8_t *rec = mxa + (static_cast<size_t>(t >> 5) * pp + (b >> 1)) * kMxARec;
-    store_hl_group8(rec, b & 1, t & 31, vh, vl);
-    if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = ok ? scale : 0.0f;
+    const uint32_t dh = pack24_group8(vh), dl = pack24_group8(vl);
+    if (r < 3) {
+      const uint32_t off = mx_dword_off(i, 3 * (g >> 2) + r);
+      *reinterpret_cast<uint32_t *>(&s_tile[j][off]) = dh;
+      *reinterpret_cast<uint32_t *>(&s_tile[j][kMxTile + off]) = dl;
+    }
+    if (g == 0) s_scale[j][i] = ok ? scale : 0.0f;
+  }
+  __syncthreads();
+  // Per half-record: 96 x 16 bytes of tiles, then the 32 scales.
+  for (int e = threadIdx.x; e < kActJobs * 128; e += kThreads) {
+    const int j = e >> 7, w = e & 127;
+    const uint32_t u = blockIdx.x * kActJobs + j;
+    if (u >= units) continue;
+    const uint32_t tt = u / bp2, b = u % bp2;
+    uint8_t *rec = mxa + (static_cast<size_t>(tt) * pp + (b >> 1)) * kMxARec;
+    if (w < 96)
+      reinterpret_cast<uint4 *>(rec + 2 * (b & 1) * kMxTile)[w] = reinterpret_cast<const uint4 *>(s_tile[j])[w];
+    else
+      reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (w - 96)] = s_scale[j][w - 96];
   }
 }
 
@@ -363,12 +382,11 @@ hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const size_t groups = mt * 32 * pp * 2;  // < 2^31: the image is below kMxMaxBytes
-  const unsigned wgs = blocks_for((groups + kActJobs - 1) / kActJobs * 8, kThreads);
-  const uint32_t stride = wgs * (kThreads / 8);
+  const size_t units = mt * pp * 2;  // half-records; < 2^31: the image is below kMxMaxBytes
+  const unsigned wgs = blocks_for(units, kActJobs);
   hipLaunchKernelGGL(act_quant_mx_kernel, dim3(wgs), dim3(kThreads), 0, st, x, static_cast<int>(m),
                      static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale,
-                     static_cast<uint32_t>(groups), stride, mxa);
+                     static_cast<uint32_t>(units), mxa);
   return hipGetLastError();
 }
 
