@@ -283,6 +283,35 @@ __device__ __forceinline__ int act_quant_group8(float4 v, bool per_row, float ro
   return static_cast<int>(__builtin_amdgcn_perm(q1, q0, 0x0c0c0400u) | __builtin_amdgcn_perm(q3, q2, 0x04000c0cu));
 }
 
+// The same quantization by a group of 4 lanes (a DPP quad): lane g holds
+// elements 8g..8g+7 of the block in a (8g..8g+3) and b (8g+4..8g+7), so the
+// per-block work (max, scale, reciprocal) is shared by 8 elements per lane
+// instead of 4.  Returns the 8 codes of the lane as two dwords (element
+// order); `scale` as act_quant_group8.
+__device__ __forceinline__ uint2 act_quant_group4(float4 a, float4 b, bool per_row, float row_scale,
+                                                  float &scale) {
+  const float ma = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+  const float mb4 = fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)));
+  uint32_t mb = __builtin_bit_cast(uint32_t, fmaxf(fmaxf(ma, mb4), 0.0f));  // never NaN, see act_quant_group8
+  mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0xB1, 0xf, 0xf, false)));
+  mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x4E, 0xf, 0xf, false)));
+  const float amax = __builtin_bit_cast(float, mb);
+  scale = per_row ? row_scale : div127_rn(amax);
+  const float inv = scale == 0.0f ? 0.0f : recip_rn(scale);
+  const float inv2 = 2.0f * inv;
+  int q[8];
+  const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (inv2 <= 0x1.fffffep127f) {  // uniform per group; false only for scale < 2^-127
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = quant_code(e[i], inv2);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = quant_code_ref(e[i], inv);
+  }
+  return make_uint2(__builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u) | __builtin_amdgcn_perm(q[3], q[2], 0x04000c0cu),
+                    __builtin_amdgcn_perm(q[5], q[4], 0x0c0c0400u) | __builtin_amdgcn_perm(q[7], q[6], 0x04000c0cu));
+}
+
 // ---- x -> LDS codes, shared by the GEMV-style kernels --------------------
 // Quantize the float4s held in registers (thread t holds x4[t + THREADS j])
 // into LDS: s_qs (natural order) and s_sa, for blocks [0, nblk).  All
@@ -327,6 +356,29 @@ __device__ __forceinline__ void quantize_regs_to_lds(const float4 (&xv)[XJ], int
                                                      float *s_sa, float *s_red) {
   const float rs = row_scale_of<THREADS, XJ>(xv, per_row, s_red);
   quant_regs<THREADS, XJ>(xv, bpr, per_row != 0, rs, s_qs, s_sa);
+}
+
+// x -> LDS codes with 4-lane groups: thread t holds the 32-byte chunks
+// t + THREADS j of x (float4s 2c and 2c + 1 of chunk c in xv[2j], xv[2j+1]),
+// so quad t / 4 + (THREADS / 4) j holds one block.  All threads must call it;
+// it ends with a barrier.
+template <int THREADS, int XP>
+__device__ __forceinline__ void quantize_pairs_to_lds(const float4 (&xv)[2 * XP], int nblk, int per_row,
+                                                      int8_t *s_qs, float *s_sa, float *s_red) {
+  const float rs = row_scale_of<THREADS, 2 * XP>(xv, per_row, s_red);
+  const int tid = threadIdx.x;
+  const int g = tid & 3;
+#pragma unroll
+  for (int j = 0; j < XP; j++) {
+    const int b = (tid >> 2) + j * (THREADS / 4);
+    if (b < nblk) {  // uniform across each quad
+      float scale;
+      const uint2 q = act_quant_group4(xv[2 * j], xv[2 * j + 1], per_row != 0, rs, scale);
+      *reinterpret_cast<uint2 *>(s_qs + b * 32 + g * 8) = q;
+      if (g == 0) s_sa[b] = scale;
+    }
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ void store_row(float *y, int row, float acc16, int mode) {

@@ -51,7 +51,13 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;  // blocks covered by the workgroup (>= bpr)
   constexpr int RG = W / KW;
-  constexpr int XJ = (KB * 8 + THREADS - 1) / THREADS;
+  // Long rows (x at least twice the workgroup's float4s) quantize in 4-lane
+  // groups of 32-byte chunks (XP per thread), which halves the per-block
+  // work per element; shorter rows keep 8-lane groups of float4s, which
+  // spreads their few blocks over twice the waves.
+  constexpr bool PAIRS = KB * 8 >= 2 * THREADS;
+  constexpr int XP = (KB * 4 + THREADS - 1) / THREADS;
+  constexpr int XJ = PAIRS ? 2 * XP : (KB * 8 + THREADS - 1) / THREADS;  // float4s of x per thread
   static_assert(W % KW == 0, "slices divide the waves");
   __shared__ __align__(16) int8_t s_qs[KB * 32];
   __shared__ float s_sa[KB];
@@ -77,7 +83,7 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   const int r = lane >> 4, c = lane & 15;
   const int kb0 = ks * 16 * BPL + c;
 
-  // (1) x: bpr*8 float4s, XJ per thread -- or (PREQ) the codes as 16-byte
+  // (1) x: XJ float4s per thread (XP chunk pairs with PAIRS) -- or (PREQ) the codes as 16-byte
   // chunks and the block scales.
   constexpr int QJ = PREQ ? (KB * 2 + THREADS - 1) / THREADS : 1;
   constexpr int SJ = PREQ ? (KB + THREADS - 1) / THREADS : 1;
@@ -93,15 +99,24 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     for (int j = 0; j < SJ; j++) sv[j] = buf_load_f32(ar, static_cast<uint32_t>(tid + j * THREADS) * 4u);
   } else {
     const auto xr = make_rsrc(a.x, static_cast<uint32_t>(bpr) * 128u);
+    if constexpr (PAIRS) {
 #pragma unroll
-    for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+      for (int j = 0; j < XP; j++) {
+        const uint32_t c = static_cast<uint32_t>(tid + j * THREADS) * 32u;
+        xv[2 * j] = buf_load_f4(xr, c);
+        xv[2 * j + 1] = buf_load_f4(xr, c + 16u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+    }
   }
 
-  // (1b) Two or more float4s of x per thread: every wave's x requests are
-  // queued before any wave's weight requests.  Without the barrier, waves
+  // (1b) x at least twice the workgroup's float4s: every wave's x requests
+  // are queued before any wave's weight requests.  Without the barrier, waves
   // that start later issue x behind the earlier waves' weight loads, and at
   // K = 8192 their x arrived up to 1.7 us after issue (0.8 us with it).
-  if constexpr (!PREQ && XJ >= 2) {
+  if constexpr (!PREQ && PAIRS) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -134,6 +149,8 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
       if (i < KB) s_sa[i] = sv[j];
     }
     __syncthreads();
+  } else if constexpr (PAIRS) {
+    quantize_pairs_to_lds<THREADS, XP>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
   } else {
     quantize_regs_to_lds<THREADS, XJ>(xv, bpr, a.per_row, s_qs, s_sa, s_red);
   }
