@@ -22,8 +22,6 @@ namespace lgh {
 
 namespace {
 
-constexpr int kThreads = 256;  // Q8_0 GEMV workgroup
-constexpr int kWaves = kThreads / kWave;
 
 struct Q4GemvArgs {
   const uint8_t *qs0;
@@ -522,73 +520,112 @@ hipError_t launch_mma(const Q4MmaArgs &a, hipStream_t st) {
 
 // ---- Q8_0 GEMV (crates/llm-engine/src/weights.rs:194-227) ---------------
 struct Q8GemvArgs {
-  const int8_t *qs;
-  const uint16_t *sc;
-  const float *x;
-  float *y;
+  const int8_t *qs;    // [n][bpr][32], natural order
+  const uint16_t *sc;  // f16 scales [n][bpr]
+  const float *x;      // [tokens][k]
+  float *y;            // [tokens][n]
   int n;
   int bpr;
-  int k;
 };
 
-// Same structure as the Q4 kernel: 2 x 128-bit loads per Q8_0 block, natural
-// order int8 weights, always per-block activation quant (weights.rs:197).
-template <int R, int S>
-__global__ __launch_bounds__(kThreads) void q8_gemv_kernel(Q8GemvArgs a) {
-  extern __shared__ __align__(16) char smem[];
+// The Q4 GEMV's mapping (one weight row per 16-lane DPP row, W waves =
+// W/KW row groups x KW K slices, lane c of a row walks blocks
+// slice*16*BPL + c + 16j) with 32-byte int8 blocks: two 128-bit loads and
+// one f16 scale per block, 8 v_dot4 against the LDS codes, and q8_apply's
+// per-block term (f32(dot) * sw) * sa added to the lane's sum
+// (weights.rs:206-212; the blocks are summed in a different order).  x is
+// always quantized per block (weights.rs:197); token blockIdx.y.
+template <int BPL, int KW, int W>
+__global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
+  constexpr int THREADS = W * kWave;
+  constexpr int KB = 16 * BPL * KW;
+  constexpr int RG = W / KW;
+  constexpr bool PAIRS = KB * 8 >= 2 * THREADS;  // as in q4_gemv_kernel
+  constexpr int XP = (KB * 4 + THREADS - 1) / THREADS;
+  constexpr int XJ = PAIRS ? 2 * XP : (KB * 8 + THREADS - 1) / THREADS;
+  static_assert(W % KW == 0, "slices divide the waves");
+  __shared__ __align__(16) int8_t s_qs[KB * 32];
+  __shared__ float s_sa[KB];
+  __shared__ float s_red[W];
+  __shared__ float s_part[KW > 1 ? RG * 4 * KW : 1];
   const int bpr = a.bpr;
-  int8_t *s_qs = reinterpret_cast<int8_t *>(smem);
-  float *s_sa = reinterpret_cast<float *>(smem + bpr * 32);
-  float *s_red = s_sa + bpr;
-  const int tok = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int row0 = (static_cast<int>(blockIdx.x) * kWaves + uniform(tid / kWave)) * R;
-  const int rows = uniform(max(0, min(R, a.n - row0)));
+  const int wave = uniform(tid / kWave);
+  const int rg = wave / KW, ks = wave % KW;
+  const int row0 = (static_cast<int>(blockIdx.x) * RG + rg) * 4;
+  const int rows = uniform(max(0, min(4, a.n - row0)));
+  const int r = lane >> 4, c = lane & 15;
+  const int kb0 = ks * 16 * BPL + c;
+  const size_t tok = blockIdx.y;
 
-  constexpr int XJ = 2 * S;
-  const auto xr = make_rsrc(a.x + static_cast<size_t>(tok) * a.k, static_cast<uint32_t>(bpr) * 128u);
+  // (1) x, then (1b) the x-before-weights barrier for long rows.
+  const auto xr = make_rsrc(a.x + tok * static_cast<size_t>(bpr) * 32, static_cast<uint32_t>(bpr) * 128u);
   float4 xv[XJ];
+  if constexpr (PAIRS) {
 #pragma unroll
-  for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * kThreads) * 16u);
+    for (int j = 0; j < XP; j++) {
+      const uint32_t off = static_cast<uint32_t>(tid + j * THREADS) * 32u;
+      xv[2 * j] = buf_load_f4(xr, off);
+      xv[2 * j + 1] = buf_load_f4(xr, off + 16u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+#pragma unroll
+    for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+  }
 
+  // (2) every weight load of this lane (rows past n fall outside the resource).
   const size_t blk0 = static_cast<size_t>(row0) * bpr;
   const auto wr = make_rsrc(a.qs + blk0 * 32, static_cast<uint32_t>(rows * bpr) * 32u);
   const auto sr = make_rsrc(a.sc + blk0, static_cast<uint32_t>(rows * bpr) * 2u);
-  uint4 w0[S][R], w1[S][R];
-  uint16_t s[S][R];
+  uint4 w0[BPL], w1[BPL];
+  uint16_t s[BPL];
 #pragma unroll
-  for (int st = 0; st < S; st++) {
-    const int kb = st * kWave + lane;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
-      w0[st][r] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u : kOOB);
-      w1[st][r] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u : kOOB);
-      s[st][r] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
-    }
+  for (int j = 0; j < BPL; j++) {
+    const int kb = kb0 + 16 * j;
+    const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
+    w0[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u : kOOB);
+    w1[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u : kOOB);
+    s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
   }
-  quantize_regs_to_lds<kThreads, XJ>(xv, bpr, 0, s_qs, s_sa, s_red);
 
-  float acc[R];
+  // (3) x -> LDS codes (per block).
+  if constexpr (PAIRS)
+    quantize_pairs_to_lds<THREADS, XP>(xv, bpr, 0, s_qs, s_sa, s_red);
+  else
+    quantize_regs_to_lds<THREADS, XJ>(xv, bpr, 0, s_qs, s_sa, s_red);
+
+  // (4) dots and terms, branch-free: a block past the row has zero weights
+  // and scale and reads block 0's codes, so its term is exactly 0.
+  float acc = 0.0f;
 #pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = 0.0f;
-#pragma unroll
-  for (int st = 0; st < S; st++) {
-    const int kb = st * kWave + lane;
-    const int kbc = kb < bpr ? kb : 0;  // past the row: zero weights and scale, adds exactly 0
+  for (int j = 0; j < BPL; j++) {
+    const int kb = kb0 + 16 * j;
+    const int kbc = kb < bpr ? kb : 0;
     const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kbc * 32);
-    const v4i a0 = ap[0], a1 = ap[1];
-    const float sa = s_sa[kbc];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-      acc[r] = fmaf(static_cast<float>(dot_q8_block(w0[st][r], w1[st][r], a0, a1)), h2f(s[st][r]) * sa, acc[r]);
+    const int d = dot_q8_block(w0[j], w1[j], ap[0], ap[1]);
+    acc += (static_cast<float>(d) * h2f(s[j])) * s_sa[kbc];
   }
-  float *y = a.y + static_cast<size_t>(tok) * a.n;
+  // (5) 16-lane row sums, slices in order, store.
+  acc += dpp<0xB1>(acc);
+  acc += dpp<0x4E>(acc);
+  acc += dpp<0x141>(acc);
+  acc += dpp<0x140>(acc);
+  float *y = a.y + tok * static_cast<size_t>(a.n);
+  if constexpr (KW == 1) {
+    if (c == 0 && r < rows) y[row0 + r] = acc;
+  } else {
+    if (c == 0) s_part[(rg * 4 + r) * KW + ks] = acc;
+    __syncthreads();
+    if (ks == 0 && lane < rows) {
+      float sum = 0.0f;
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    const float t = wave_sum_dpp(acc[r]);
-    if (lane == 0 && r < rows) y[row0 + r] = t;
+      for (int k = 0; k < KW; k++) sum += s_part[(rg * 4 + lane) * KW + k];
+      y[row0 + lane] = sum;
+    }
   }
 }
 
@@ -597,7 +634,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(Q8GemvArgs a) {
 // Q4 GEMV plan: KW K slices of 64 blocks per workgroup cover the row
 // (K <= 64*32*16 = 32768), then rows per wave R so the launch has >= ~4096
 // waves while every lane keeps its R weight loads in registers.
-Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat) {
+Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
   Q4GemvPlan p{};
   if (bpr <= 64) {  // one slice: 16 lanes x BPL blocks cover the row
     p.KW = 1;
@@ -610,9 +647,20 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat) {
   p.ok = static_cast<size_t>(16 * p.BPL * p.KW) >= bpr;
   // Waves per workgroup: the largest of 16 / 8 / 4 (>= KW) that still gives
   // >= 192 workgroups; every workgroup re-quantizes all of x, so fewer and
-  // larger workgroups win as long as most CUs stay busy.
+  // larger workgroups win as long as most CUs stay busy.  With `narrow`, 8
+  // rather than 16 once 8 gives two or more workgroups per CU (measured
+  // against 16: the Q4 N=65536 head 10.9 -> 10.4 us, the gate/up pair
+  // 4.58 -> 4.41 us; the Q8_0 head 19.2 -> 19.8 us, so it keeps 16).
   p.W = 16;
   while (p.W > 4 && p.W > p.KW && n * nmat / static_cast<size_t>(4 * p.W / p.KW) < 192) p.W >>= 1;
+  if (narrow && p.W == 16 && p.KW <= 8 && n * nmat * static_cast<size_t>(p.KW) / 32 >= 512) p.W = 8;
+  // Without `narrow` (Q8_0 rows), short rows that leave < 192 workgroups even
+  // at 4 waves take two K slices (K=N=1536: 96 -> 192 workgroups, 3.43 ->
+  // 2.46 us; Q4 rows of the same shape measured no change).
+  if (!narrow && p.KW == 1 && p.W == 4 && bpr > 16 && n * nmat / 16 < 192) {
+    p.KW = 2;
+    p.BPL = static_cast<int>((bpr + 31) / 32);
+  }
   const int rows_per_wg = 4 * p.W / p.KW;
   p.wgs_per_mat = static_cast<int>((n + rows_per_wg - 1) / rows_per_wg);
   return p;
@@ -758,40 +806,41 @@ hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float
   return hipErrorInvalidValue;
 }
 
-// Rows per wave for the Q8_0 GEMV.
-static int pick_rows_per_wave(size_t n_total, int steps) {
-  int r = 8;
-  while (r > 1 && (n_total / static_cast<size_t>(r)) < 2048) r >>= 1;
-  while (r > 1 && r * steps > 8) r >>= 1;
-  return r;
-}
-
+// The Q8_0 GEMV takes the Q4 GEMV's plan (same row mapping, same limits).
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens, hipStream_t st) {
   if (w->n == 0 || tokens == 0) return hipSuccess;
-  Q8GemvArgs a{w->qs, w->sc, x, y, static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(w->k)};
-  const size_t smem = w->bpr * 36 + kWaves * sizeof(float);
-  const int steps = static_cast<int>((w->bpr + kWave - 1) / kWave);
-  const int R = pick_rows_per_wave(w->n * tokens, steps) >= 2 ? 2 : 1;
-  const dim3 grid(static_cast<unsigned>((w->n + kWaves * R - 1) / (kWaves * R)), static_cast<unsigned>(tokens));
-#define LGH_Q8(RR, SS)                                                                      \
-  if (R == RR && steps == SS) {                                                             \
-    hipLaunchKernelGGL((q8_gemv_kernel<RR, SS>), grid, dim3(kThreads), smem, st, a);        \
+  const Q4GemvPlan p = plan_q4_gemv(w->n, w->bpr, 1, false);
+  if (!p.ok || tokens > 65535) return hipErrorInvalidValue;  // rejected by the API before launch
+  Q8GemvArgs a{w->qs, w->sc, x, y, static_cast<int>(w->n), static_cast<int>(w->bpr)};
+  const dim3 grid(static_cast<unsigned>(p.wgs_per_mat), static_cast<unsigned>(tokens));
+#define LGH_Q8(BB, KK, WW)                                                                  \
+  if (p.BPL == BB && p.KW == KK && p.W == WW) {                                             \
+    hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW>), grid, dim3(WW * kWave), 0, st, a);      \
     return hipGetLastError();                                                               \
   }
-  LGH_Q8(2, 1);
-  LGH_Q8(1, 1);
-  LGH_Q8(2, 2);
-  LGH_Q8(1, 2);
-  LGH_Q8(1, 3);
-  LGH_Q8(1, 4);
-  LGH_Q8(2, 3);
-  LGH_Q8(2, 4);
-  LGH_Q8(1, 5);
-  LGH_Q8(1, 6);
-  LGH_Q8(2, 5);
-  LGH_Q8(2, 6);
+  LGH_Q8(1, 1, 16);
+  LGH_Q8(1, 1, 8);
+  LGH_Q8(1, 1, 4);
+  LGH_Q8(2, 1, 16);
+  LGH_Q8(2, 1, 8);
+  LGH_Q8(2, 1, 4);
+  LGH_Q8(3, 1, 16);
+  LGH_Q8(3, 1, 8);
+  LGH_Q8(3, 1, 4);
+  LGH_Q8(4, 1, 16);
+  LGH_Q8(4, 1, 8);
+  LGH_Q8(4, 1, 4);
+  LGH_Q8(2, 4, 16);
+  LGH_Q8(2, 4, 8);
+  LGH_Q8(2, 4, 4);
+  LGH_Q8(2, 8, 16);
+  LGH_Q8(2, 8, 8);
+  LGH_Q8(2, 16, 16);
+  LGH_Q8(4, 16, 16);
+  LGH_Q8(1, 2, 4);
+  LGH_Q8(2, 2, 4);
 #undef LGH_Q8
-  return hipErrorInvalidValue;  // K > 12288: rejected by the API before launch
+  return hipErrorInvalidValue;
 }
 
 }  // namespace lgh

@@ -112,7 +112,9 @@ struct Q4GemvPlan {
   int BPL, KW, W, wgs_per_mat;
   bool ok;
 };
-Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat);
+// narrow: prefer 8-wave workgroups once that gives >= 2 per CU (Q4 rows;
+// the Q8_0 head's 2x wider rows ran faster with 16 waves).
+Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow = true);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);
 // FFN gate/up stage of one decode token (lgh_ffn.hip): RMSNorm of x with
@@ -164,8 +166,8 @@ hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row,
                                 float *row_scale, hipStream_t stream);
 hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
                               int mode, hipStream_t stream);
-// Q8_0 GEMV for k <= kQ8GemvMaxK.
-constexpr size_t kQ8GemvMaxK = 12288;
+// Q8_0 GEMV for k <= kQ8GemvMaxK (the Q4 GEMV plan's reach).
+constexpr size_t kQ8GemvMaxK = 32768;
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens,
                           hipStream_t stream);
 

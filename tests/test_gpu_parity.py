@@ -408,14 +408,24 @@ def test_gemm_add_and_per_row(gpu_ctx, oracle, per_row):
 
 
 # ---- Q8_0 GEMV ---------------------------------------------------------------------------
-@pytest.mark.parametrize("n,k,tokens", [(1536, 1536, 1), (77, 256, 3), (4096, 1536, 2)])
+@pytest.mark.parametrize("n,k,tokens", [(1536, 1536, 1), (77, 256, 3), (4096, 1536, 2), (65536, 1536, 1),
+                                         (300, 4096, 2), (70, 8192, 1), (33, 16384, 1), (20, 32768, 2),
+                                         (5, 32, 3), (1, 64, 1), (130, 96, 4)])
 def test_q8_gemv_matches_oracle(gpu_ctx, oracle, n, k, tokens):
+    """Every plan of the Q8_0 GEMV: one K slice (1..4 blocks per lane), 4 / 8 / 16 slices,
+    rows not a multiple of 4, several tokens (grid.y), the N=65536 head."""
     blocks = synth.q8_blocks(n + k, n, k)
     x = synth.activations(tokens + k, tokens, k)
     w = q4.Q8Matrix.from_blocks(n, k, blocks, gpu_ctx)
     got = np.zeros((tokens, n) if tokens > 1 else n, dtype=np.float32)
     q4.q8_apply(w, x, tokens, got)
     assert_close(got, oracle.q8_apply(blocks, n, k, x, tokens, threads=8), what="q8")
+
+
+def test_q8_gemv_rejects_long_rows(gpu_ctx):
+    w = q4.Q8Matrix.from_blocks(2, 32 * 1025, synth.q8_blocks(9, 2, 32 * 1025), gpu_ctx)
+    with pytest.raises(q4.LghShapeError, match="32768"):
+        q4.q8_apply(w, np.zeros(32 * 1025, np.float32), 1, np.zeros(2, np.float32))
 
 
 # ---- error behaviour --------------------------------------------------------------------------
