@@ -210,7 +210,8 @@ def q8_case(gb: GpuBench, iters, n=1536, k=1536):
 
 
 def q4_head_case(gb: GpuBench, iters, n=65536, k=1536):
-    """Q4 GEMV at the tied-head shape (the alternative to the Q8_0 head)."""
+    """Q4 GEMV over rotating copies (> 2x MALL); default: the tied-head shape (the alternative to
+    the Q8_0 head)."""
     torch, q4 = gb.torch, gb.q4
     from llmhost_amd import synth
 
@@ -409,6 +410,11 @@ def main():
         log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
         extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
         extra["q4_head_k1536_n65536"] = q4_head_case(gb, 20)
+        log("[bench] Q4 GEMV size sweep (launch floor -> HBM bound)")
+        extra["q4_gemv_size_sweep"] = [
+            {k: round(v, 3) if isinstance(v, float) else v for k, v in q4_head_case(gb, 40, n, k).items()}
+            for (n, k) in ((8192, 1536), (16384, 1536), (32768, 1536), (65536, 1536), (131072, 1536),
+                           (1536, 8192), (4096, 8192), (16384, 8192))]
         log("[bench] decode FFN block (fused vs per-op)")
         extra["ffn_block_dim1536_inter8192"] = ffn_case(gb, 100)
     cpu = None

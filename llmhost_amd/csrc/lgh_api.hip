@@ -374,6 +374,18 @@ static int launch_gemv(lgh_ctx *ctx, const lgh_q4 *w0, float *y0, const lgh_q4 *
     return w1 ? lgh_q4_gemm_dev(ctx, w1, x, y1, 1, mode) : LGH_OK;
   }
   if (int r = set_device(ctx)) return r;
+  if (lgh::q4_gemv_quantize_once(w0->n, w0->bpr, w1 ? 2 : 1)) {
+    Carve cv;
+    const size_t oq = cv.take(w0->k), os = cv.take(w0->bpr * sizeof(float)), orow = cv.take(sizeof(float));
+    if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
+    char *ws = static_cast<char *>(ctx->ws);
+    auto *qs = reinterpret_cast<int8_t *>(ws + oq);
+    auto *sc = reinterpret_cast<float *>(ws + os);
+    LGH_HIP(ctx, lgh::launch_act_quant(x, 1, w0->k, ctx->act_mode, qs, sc, nullptr,
+                                       reinterpret_cast<float *>(ws + orow), ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemv_any(w0, y0, w1, y1, nullptr, qs, sc, mode, 0, ctx->stream));
+    return LGH_OK;
+  }
   LGH_HIP(ctx, lgh::launch_q4_gemv(w0, y0, w1, y1, x, mode, ctx->act_mode, ctx->stream));
   return LGH_OK;
 }

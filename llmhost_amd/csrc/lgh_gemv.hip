@@ -647,13 +647,21 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
   p.ok = static_cast<size_t>(16 * p.BPL * p.KW) >= bpr;
   // Waves per workgroup: the largest of 16 / 8 / 4 (>= KW) that still gives
   // >= 192 workgroups; every workgroup re-quantizes all of x, so fewer and
-  // larger workgroups win as long as most CUs stay busy.  With `narrow`, 8
-  // rather than 16 once 8 gives two or more workgroups per CU (measured
-  // against 16: the Q4 N=65536 head 10.9 -> 10.4 us, the gate/up pair
-  // 4.58 -> 4.41 us; the Q8_0 head 19.2 -> 19.8 us, so it keeps 16).
+  // larger workgroups win as long as most CUs stay busy.
   p.W = 16;
   while (p.W > 4 && p.W > p.KW && n * nmat / static_cast<size_t>(4 * p.W / p.KW) < 192) p.W >>= 1;
-  if (narrow && p.W == 16 && p.KW <= 8 && n * nmat * static_cast<size_t>(p.KW) / 32 >= 512) p.W = 8;
+  // Long rows: twice the blocks per lane and half the slices (twice the rows
+  // per workgroup, half the workgroups re-quantizing x) while >= 512
+  // workgroups remain (K=8192: N=16384 19.9 -> 14.9 us, N=4096 6.4 -> 5.5 us).
+  while (p.W == 16 && p.KW >= 8 && p.BPL < 4 && n * nmat * static_cast<size_t>(p.KW / 2) / 64 >= 512) {
+    p.KW /= 2;
+    p.BPL *= 2;
+  }
+  // One slice, `narrow`: 8 rather than 16 waves once 8 gives two or more
+  // workgroups per CU (measured against 16: the Q4 N=65536 head 10.9 ->
+  // 10.4 us, the gate/up pair 4.58 -> 4.41 us; the Q8_0 head 19.2 -> 19.8 us,
+  // so it keeps 16).
+  if (narrow && p.W == 16 && p.KW == 1 && n * nmat / 32 >= 512) p.W = 8;
   // Without `narrow` (Q8_0 rows), short rows that leave < 192 workgroups even
   // at 4 waves take two K slices (K=N=1536: 96 -> 192 workgroups, 3.43 ->
   // 2.46 us; Q4 rows of the same shape measured no change).
@@ -664,6 +672,14 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
   const int rows_per_wg = 4 * p.W / p.KW;
   p.wgs_per_mat = static_cast<int>((n + rows_per_wg - 1) / rows_per_wg);
   return p;
+}
+
+// Quantize x once (act_quant_kernel) and run the codes GEMV instead when
+// the workgroups would re-quantize more than ~12M elements of x between them
+// (K=16384, N=8192: 19.5 -> 15.9 us; K=8192, N=16384 is even at 8.4M).
+bool q4_gemv_quantize_once(size_t n, size_t bpr, int nmat) {
+  const Q4GemvPlan p = plan_q4_gemv(n, bpr, nmat);
+  return p.ok && static_cast<size_t>(p.wgs_per_mat) * nmat * bpr * 32 >= (size_t{12} << 20);
 }
 
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x, int mode,
@@ -721,6 +737,8 @@ hipError_t launch_q4_gemv_any(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, flo
   LGH_G16(2, 8, 8);
   LGH_G16(2, 16, 16);
   LGH_G16(4, 16, 16);
+  LGH_G16(4, 4, 16);
+  LGH_G16(4, 8, 16);
 #undef LGH_G16
   return hipErrorInvalidValue;
 }
@@ -837,6 +855,8 @@ hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t toke
   LGH_Q8(2, 8, 8);
   LGH_Q8(2, 16, 16);
   LGH_Q8(4, 16, 16);
+  LGH_Q8(4, 4, 16);
+  LGH_Q8(4, 8, 16);
   LGH_Q8(1, 2, 4);
   LGH_Q8(2, 2, 4);
 #undef LGH_Q8

@@ -115,6 +115,7 @@ struct Q4GemvPlan {
 // narrow: prefer 8-wave workgroups once that gives >= 2 per CU (Q4 rows;
 // the Q8_0 head's 2x wider rows ran faster with 16 waves).
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow = true);
+bool q4_gemv_quantize_once(size_t n, size_t bpr, int nmat);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);
 // FFN gate/up stage of one decode token (lgh_ffn.hip): RMSNorm of x with

@@ -331,6 +331,50 @@ def test_gemv_pair(gpu_ctx, oracle):
     assert np.array_equal(og, sg)
 
 
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("n,k", [(8192, 16384), (16384, 8192), (4096, 8192)])
+def test_gemv_long_rows_at_large_n(gpu_ctx, oracle, n, k, per_row):
+    """The plans for long rows at large N: more rows per workgroup (K=8192), and past ~12M
+    re-quantized elements (K=16384, N=8192) x quantized once then the codes GEMV.
+    Assign and AddF64, both act-quant modes."""
+    blocks = synth.q4_blocks(n + k, n, k)
+    x = synth.normal_f32(n + 2, k)
+    y0 = synth.normal_f32(n + 3, n)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        got = np.zeros(n, dtype=np.float32)
+        q4.gemv_q4(w, x, got)
+        add = y0.copy()
+        q4.gemv_q4_add(w, x, add)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    assert_close(got, oracle.gemv_q4(mat, x, per_row=per_row, threads=8), what="assign")
+    assert_close(add, oracle.gemv_q4(mat, x, out=y0.copy(), add=True, per_row=per_row, threads=8), what="add")
+    w.free()
+
+
+def test_gemv_pair_long_rows_equals_two_gemvs(gpu_ctx, oracle):
+    """A pair at K=16384 takes the quantize-once route, each single GEMV the in-kernel one:
+    the codes are the same, so the results are bit-identical."""
+    n, k = 4096, 16384
+    bg, bu = synth.q4_blocks(51, n, k), synth.q4_blocks(52, n, k)
+    x = synth.normal_f32(53, k)
+    wg, wu = q4.Q4Matrix.from_blocks(n, k, bg, gpu_ctx), q4.Q4Matrix.from_blocks(n, k, bu, gpu_ctx)
+    og, ou = np.zeros(n, dtype=np.float32), np.zeros(n, dtype=np.float32)
+    q4.gemv_q4_pair(wg, wu, x, og, ou)
+    rg, ru = oracle.gemv_q4_pair(oracle.Q4Matrix(n, k, bg), oracle.Q4Matrix(n, k, bu), x, threads=8)
+    assert_close(og, rg, what="gate")
+    assert_close(ou, ru, what="up")
+    sg, su = np.zeros(n, dtype=np.float32), np.zeros(n, dtype=np.float32)
+    q4.gemv_q4(wg, x, sg)
+    q4.gemv_q4(wu, x, su)
+    assert np.array_equal(og, sg) and np.array_equal(ou, su)
+    wg.free()
+    wu.free()
+
+
 # ---- GEMM -----------------------------------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(2, 48, 64), (4, 8192, 2048), (16, 512, 2048), (20, 48, 64),
                                    (40, 48, 64), (64, 1000, 2048), (100, 257, 320), (512, 256, 2048),
