@@ -158,21 +158,31 @@ __device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, i
                                               float (&acc)[TN][TM][16]) {
   const int lane = threadIdx.x & 63, row = lane & 31, half = lane >> 5;
   const v32f zero32 = {};
-  // Scale inputs of the outer products: lane L holds block L/32, row or token
-  // L%32 -- the record's f32 scale array [block][row] read linearly.
+  // The scale outer products go first: lane L holds block L/32, row or token
+  // L%32 of the record's f32 scale array [block][row] (read linearly).  Their
+  // 16-pass MFMA runs while the dot operands arrive from LDS, and their
+  // result is ready when the first block's dots are.
   float xs[TN], ys[TM];
   v8i A[2][TN], B[2][TM];
 #pragma unroll
+  for (int tn = 0; tn < TN; tn++) xs[tn] = reinterpret_cast<const float *>(buf + (wn * TN + tn) * kWRec + 2 * kTile)[lane];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+    ys[tm] = reinterpret_cast<const float *>(buf + C::A_LDS + (wm * TM + tm) * kARec + 4 * kTile)[lane];
+  v32f P[TN][TM];
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) P[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x1f32(xs[tn], ys[tm], zero32, 0, 0, 0);
+#pragma unroll
   for (int tn = 0; tn < TN; tn++) {
     const char *rec = buf + (wn * TN + tn) * kWRec;
-    xs[tn] = reinterpret_cast<const float *>(rec + 2 * kTile)[lane];
     A[0][tn] = mx_row(rec, row);
     A[1][tn] = mx_row_at(rec + kTile, r16, r8);
   }
 #pragma unroll
   for (int tm = 0; tm < TM; tm++) {
     const char *rec = buf + C::A_LDS + (wm * TM + tm) * kARec;
-    ys[tm] = reinterpret_cast<const float *>(rec + 4 * kTile)[lane];
     B[0][tm] = mx_row(rec + half * kTile, row);
     B[1][tm] = mx_row_at(rec + (2 + half) * kTile, r16, r8);
   }
@@ -180,22 +190,22 @@ __device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, i
   for (int tn = 0; tn < TN; tn++)
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
-      const v32f P = __builtin_amdgcn_mfma_f32_32x32x1f32(xs[tn], ys[tm], zero32, 0, 0, 0);
       const v16f c0 = mx_block_dot(A[0][tn], B[0][tm]);
       const v16f c1 = mx_block_dot(A[1][tn], B[1][tm]);
-      // Both blocks' dots are issued before either is folded (the second
-      // block's MFMA overlaps the first block's folds); per element the
-      // blocks are added in order.
+      // Per element the blocks are added in order.
       float t0[16];
 #pragma unroll
-      for (int v = 0; v < 16; v++) t0[v] = fmaf(c0[v], P[v], acc[tn][tm][v]);
+      for (int v = 0; v < 16; v++) t0[v] = fmaf(c0[v], P[tn][tm][v], acc[tn][tm][v]);
 #pragma unroll
-      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c1[v], P[16 + v], t0[v]);
+      for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c1[v], P[tn][tm][16 + v], t0[v]);
     }
+  __builtin_amdgcn_sched_group_barrier(0x100, TN + TM, 0);        // DS reads of the scales
+  __builtin_amdgcn_sched_group_barrier(0x008, TN * TM, 0);        // outer products
+  __builtin_amdgcn_sched_group_barrier(0x100, 4 * (TN + TM), 0);  // DS reads of the operands
 #pragma unroll
   for (int t = 0; t < TN * TM; t++) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);  // VALU
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // block dots
+    __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);  // folds
   }
 }
 
