@@ -371,6 +371,23 @@ def measured_traffic(name: str):
     return None
 
 
+KTRACE_FILE = os.path.join(ROOT, "profiles", "q4_gemv_up_down_k1536_n8192_kernel_trace.md")
+
+
+def rocprof_avg_us(name: str):
+    """Average kernel duration (us) of the headline GEMV `name` in the committed
+    rocprofv3 kernel trace of `bench.py --quick`, or None."""
+    try:
+        with open(KTRACE_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 3 and parts[0] == "rocprof_avg_us" and parts[1] == name:
+                    return float(parts[2])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -440,7 +457,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": f"q4_gemv ({dom_name}: K={dom['k']}, N={dom['n']})",
                      "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
-                     "bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3)},
+                     "bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3),
+                     "rocprof_avg_us": rocprof_avg_us(dom_name)},
         "cpu_baseline": cpu,
         "extra": extra,
     }
