@@ -43,9 +43,13 @@ extern "C" {
 #define LGH_ERR_NO_DEVICE (-5)   /* no such HIP device                         */
 #define LGH_ERR_OOM (-6)         /* device or host allocation failed           */
 
-/* Accumulation mode, crates/llm-cpu/src/gemv_q4.rs:445-449 AccMode. */
+/* Accumulation mode, crates/llm-cpu/src/gemv_q4.rs:445-449 AccMode, plus the
+ * f32 residual add the attention and conv blocks apply after their output
+ * projection (Linear::apply then add_inplace, crates/llm-cpu/src/ops.rs:48-53;
+ * crates/llm-engine/src/lfm2.rs:645, 682, 749, 857). */
 #define LGH_ASSIGN 0  /* out = W x                                  */
 #define LGH_ADD_F64 1 /* out = (float)((double)out + (double)(W x)) */
+#define LGH_ADD_F32 2 /* out = out + (float)(W x), in f32           */
 
 /* Activation quantization, crates/llm-cpu/src/gemv_q4.rs:263-271 ActQuant. */
 #define LGH_ACT_PER_BLOCK 0 /* one scale per 32-element block (default) */
@@ -188,6 +192,23 @@ int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const 
                         const float *norm_w, float eps, float *hidden, size_t tokens);
 int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
                             const float *norm_w_dev, float eps, float *hidden_dev, size_t tokens);
+
+/* ---- attention / conv block input side ----------------------------------------
+ * rms_norm, then the block's input projections, all on the same normed rows,
+ * over `tokens` rows of hidden [tokens, k]:
+ *   normed = rms_norm(hidden, norm_w, eps)   (norm_w == NULL: normed = hidden)
+ *   y[j]   = W[j] normed  (mode as lgh_q4_gemm), j < nmat, 1 <= nmat <= 3
+ * -- Lfm2::attn_decode's q_proj / k_proj / v_proj (crates/llm-engine/src/
+ * lfm2.rs:784-794) and Lfm2::conv_update's in_proj (lfm2.rs:651-659); prefill
+ * alike (lfm2.rs:698-711, and 609-625 when no position is padding).  Every W[j] has the same k; y[j] is
+ * [tokens, W[j].n].  One token with k <= 2048 runs one launch: the norm in
+ * its prologue and one activation quantization shared by all matrices (as
+ * gemv_q4_pair shares one, crates/llm-cpu/src/gemv_q4.rs:396-443); otherwise
+ * rms_norm then one lgh_q4_gemm per matrix.  Results equal that sequence. */
+int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,
+                     const float *hidden, float *const *y, size_t tokens, int mode);
+int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w_dev, float eps,
+                         const float *hidden_dev, float *const *y_dev, size_t tokens, int mode);
 
 /* ---- test hooks (host pointers, synchronous) -------------------------------
  * ActQ8::quantize / quantize_row / quantize_batch (gemv_q4.rs:33-95,

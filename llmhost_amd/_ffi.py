@@ -23,6 +23,7 @@ LGH_ERR_OOM = -6
 
 LGH_ASSIGN = 0
 LGH_ADD_F64 = 1
+LGH_ADD_F32 = 2
 LGH_ACT_PER_BLOCK = 0
 LGH_ACT_PER_ROW = 1
 
@@ -76,6 +77,8 @@ SIGNATURES = {
     "lgh_q4_ffn_residual": (_I, [_P, _P, _P, _P, _P, C.c_float, _P, _SZ]),
     "lgh_q4_ffn_residual_dev": (_I, [_P, _P, _P, _P, _P, C.c_float, _P, _SZ]),
     "lgh_q4_ffn_gate_up": (_I, [_P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _P, _P]),
+    "lgh_q4_norm_gemv": (_I, [_P, _SZ, _P, _P, C.c_float, _P, _P, _SZ, _I]),
+    "lgh_q4_norm_gemv_dev": (_I, [_P, _SZ, _P, _P, C.c_float, _P, _P, _SZ, _I]),
 }
 
 _lib = None

@@ -359,7 +359,7 @@ size_t lgh_q8_cols(const lgh_q8 *w) { return w ? w->k : 0; }
 
 // ---- device-pointer entry points -------------------------------------------
 static int check_mode(lgh_ctx *ctx, int mode) {
-  if (mode != LGH_ASSIGN && mode != LGH_ADD_F64)
+  if (mode != LGH_ASSIGN && mode != LGH_ADD_F64 && mode != LGH_ADD_F32)
     return fail(ctx, LGH_ERR_INVALID_ARG, "unknown accumulation mode %d", mode);
   return LGH_OK;
 }
@@ -448,7 +448,7 @@ int lgh_q4_gemv_prep(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, const floa
   auto *yd = reinterpret_cast<float *>(st + oy);
   if (qb) LGH_HIP(ctx, hipMemcpyAsync(qd, qs, qb, hipMemcpyHostToDevice, ctx->stream));
   if (sb) LGH_HIP(ctx, hipMemcpyAsync(sd, scales, sb, hipMemcpyHostToDevice, ctx->stream));
-  if (mode == LGH_ADD_F64) LGH_HIP(ctx, hipMemcpyAsync(yd, y, yb, hipMemcpyHostToDevice, ctx->stream));
+  if (mode != LGH_ASSIGN) LGH_HIP(ctx, hipMemcpyAsync(yd, y, yb, hipMemcpyHostToDevice, ctx->stream));
   if (int r = lgh_q4_gemv_prep_dev(ctx, w, qd, sd, yd, mode)) return r;
   LGH_HIP(ctx, hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -564,7 +564,7 @@ int lgh_q4_gemm(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, size_t 
   char *st = static_cast<char *>(ctx->stage);
   float *xd = reinterpret_cast<float *>(st + ox), *yd = reinterpret_cast<float *>(st + oy);
   LGH_HIP(ctx, hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
-  if (mode == LGH_ADD_F64) LGH_HIP(ctx, hipMemcpyAsync(yd, y, yb, hipMemcpyHostToDevice, ctx->stream));
+  if (mode != LGH_ASSIGN) LGH_HIP(ctx, hipMemcpyAsync(yd, y, yb, hipMemcpyHostToDevice, ctx->stream));
   if (int r = lgh_q4_gemm_dev(ctx, w, xd, yd, m, mode)) return r;
   LGH_HIP(ctx, hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -764,6 +764,90 @@ int lgh_q4_ffn_gate_up(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const f
   LGH_HIP(ctx, hipMemcpyAsync(h, hd, yb, hipMemcpyDeviceToHost, ctx->stream));
   if (hq) LGH_HIP(ctx, hipMemcpyAsync(hq, qd, n, hipMemcpyDeviceToHost, ctx->stream));
   if (hs) LGH_HIP(ctx, hipMemcpyAsync(hs, sd, n / 32 * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+// ---- attention / conv block input side -------------------------------------
+static int check_multi(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w) {
+  if (!w || nmat < 1 || nmat > 3) return fail(ctx, LGH_ERR_INVALID_ARG, "need 1 to 3 matrices, got %zu", nmat);
+  for (size_t j = 0; j < nmat; j++) {
+    if (!w[j]) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix %zu", j);
+    if (w[j]->k != w[0]->k)
+      return fail(ctx, LGH_ERR_SHAPE, "matrix %zu has k = %zu, matrix 0 k = %zu", j, w[j]->k, w[0]->k);
+  }
+  return LGH_OK;
+}
+
+int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w_dev, float eps,
+                         const float *hidden_dev, float *const *y_dev, size_t tokens, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (int r = check_multi(ctx, nmat, w)) return r;
+  if (int r = check_mode(ctx, mode)) return r;
+  const int nm = static_cast<int>(nmat);
+  const size_t rows = lgh::gemv_multi_rows(w, nm), k = w[0]->k;
+  if (tokens == 0 || rows == 0) return LGH_OK;
+  if (!y_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null output array");
+  for (size_t j = 0; j < nmat; j++)
+    if (w[j]->n && !y_dev[j]) return fail(ctx, LGH_ERR_INVALID_ARG, "null output %zu", j);
+  if (k && !hidden_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
+  if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "hidden and norm weight must be 16-byte aligned");
+  if (int r = set_device(ctx)) return r;
+  // One token whose rows fit one K slice: a single launch (norm in the
+  // prologue, one act-quant shared by every matrix).
+  if (tokens == 1 && k > 0 && w[0]->bpr <= lgh::kFfnMaxBpr && lgh::plan_q4_gemv(rows, w[0]->bpr, 1).ok &&
+      !lgh::q4_gemv_quantize_once(rows, w[0]->bpr, 1)) {
+    LGH_HIP(ctx, lgh::launch_q4_gemv_multi(w, y_dev, nm, hidden_dev, nullptr, nullptr, norm_w_dev, eps, mode,
+                                           ctx->act_mode, ctx->stream));
+    return LGH_OK;
+  }
+  // Otherwise the reference's sequence (rms_norm, then one apply per matrix).
+  const float *normed = hidden_dev;
+  if (norm_w_dev && k) {
+    if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, tokens * k * sizeof(float))) return r;
+    float *nd = static_cast<float *>(ctx->ffn);
+    LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, k, tokens, eps, nd, ctx->stream));
+    normed = nd;
+  }
+  for (size_t j = 0; j < nmat; j++)
+    if (int r = lgh_q4_gemm_dev(ctx, w[j], normed, y_dev[j], tokens, mode)) return r;
+  return LGH_OK;
+}
+
+int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,
+                     const float *hidden, float *const *y, size_t tokens, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (int r = check_multi(ctx, nmat, w)) return r;
+  if (int r = check_mode(ctx, mode)) return r;
+  const size_t rows = lgh::gemv_multi_rows(w, static_cast<int>(nmat)), k = w[0]->k;
+  if (tokens == 0 || rows == 0) return LGH_OK;
+  if (!y) return fail(ctx, LGH_ERR_INVALID_ARG, "null output array");
+  for (size_t j = 0; j < nmat; j++)
+    if (w[j]->n && !y[j]) return fail(ctx, LGH_ERR_INVALID_ARG, "null output %zu", j);
+  if (k && !hidden) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = tokens * k * sizeof(float), nb = k * sizeof(float);
+  const size_t ox = cv.take(xb), on = cv.take(norm_w ? nb : 0);
+  size_t oy[3] = {0, 0, 0};
+  for (size_t j = 0; j < nmat; j++) oy[j] = cv.take(tokens * w[j]->n * sizeof(float));
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *nd = norm_w ? reinterpret_cast<float *>(st + on) : nullptr;
+  float *yd[3] = {nullptr, nullptr, nullptr};
+  if (k) LGH_HIP(ctx, hipMemcpyAsync(xd, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (norm_w && k) LGH_HIP(ctx, hipMemcpyAsync(nd, norm_w, nb, hipMemcpyHostToDevice, ctx->stream));
+  for (size_t j = 0; j < nmat; j++) {
+    yd[j] = reinterpret_cast<float *>(st + oy[j]);
+    const size_t yb = tokens * w[j]->n * sizeof(float);
+    if (mode != LGH_ASSIGN && yb) LGH_HIP(ctx, hipMemcpyAsync(yd[j], y[j], yb, hipMemcpyHostToDevice, ctx->stream));
+  }
+  if (int r = lgh_q4_norm_gemv_dev(ctx, nmat, w, nd, eps, xd, yd, tokens, mode)) return r;
+  for (size_t j = 0; j < nmat; j++) {
+    const size_t yb = tokens * w[j]->n * sizeof(float);
+    if (yb) LGH_HIP(ctx, hipMemcpyAsync(y[j], yd[j], yb, hipMemcpyDeviceToHost, ctx->stream));
+  }
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return LGH_OK;
 }

@@ -381,12 +381,18 @@ __device__ __forceinline__ void quantize_pairs_to_lds(const float4 (&xv)[2 * XP]
   __syncthreads();
 }
 
+// The caller's accumulation mode applied to one output: Assign, AddF64
+// (gemv_q4.rs:486-497) or the f32 residual add (ops.rs:48-53 add_inplace
+// after an Assign).
+__device__ __forceinline__ float apply_mode(float old, float v, int mode) {
+  if (mode == LGH_ADD_F64) return static_cast<float>(static_cast<double>(old) + static_cast<double>(v));
+  if (mode == LGH_ADD_F32) return old + v;
+  return v;
+}
+
 __device__ __forceinline__ void store_row(float *y, int row, float acc16, int mode) {
   const float v = acc16 * 0.0625f;  // exact: undo the x16 of the nibble unpack
-  if (mode == LGH_ADD_F64)
-    y[row] = static_cast<float>(static_cast<double>(y[row]) + static_cast<double>(v));
-  else
-    y[row] = v;
+  y[row] = mode == LGH_ASSIGN ? v : apply_mode(y[row], v, mode);
 }
 
 // ---- MX-fp6 operand codes ----------------------------------------------------

@@ -300,22 +300,19 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
         float v[4] = {acc[tn][tm][4 * q], acc[tn][tm][4 * q + 1], acc[tn][tm][4 * q + 2], acc[tn][tm][4 * q + 3]};
         if (vec4 && i0 + 3 < g.n) {
           float4 *dst = reinterpret_cast<float4 *>(yrow + i0);
-          if (mode == LGH_ADD_F64) {
+          if (mode != LGH_ASSIGN) {
             const float4 o = *dst;
-            v[0] = static_cast<float>(static_cast<double>(o.x) + static_cast<double>(v[0]));
-            v[1] = static_cast<float>(static_cast<double>(o.y) + static_cast<double>(v[1]));
-            v[2] = static_cast<float>(static_cast<double>(o.z) + static_cast<double>(v[2]));
-            v[3] = static_cast<float>(static_cast<double>(o.w) + static_cast<double>(v[3]));
+            v[0] = apply_mode(o.x, v[0], mode);
+            v[1] = apply_mode(o.y, v[1], mode);
+            v[2] = apply_mode(o.z, v[2], mode);
+            v[3] = apply_mode(o.w, v[3], mode);
           }
           *dst = make_float4(v[0], v[1], v[2], v[3]);
         } else {
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             if (i0 + e >= g.n) continue;
-            if (mode == LGH_ADD_F64)
-              yrow[i0 + e] = static_cast<float>(static_cast<double>(yrow[i0 + e]) + static_cast<double>(v[e]));
-            else
-              yrow[i0 + e] = v[e];
+            yrow[i0 + e] = mode == LGH_ASSIGN ? v[e] : apply_mode(yrow[i0 + e], v[e], mode);
           }
         }
       }
@@ -348,7 +345,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   if (i >= total) return;
   float v = part[i];
   for (int z = 1; z < splits; z++) v += part[static_cast<size_t>(z) * total + i];
-  y[i] = mode == LGH_ADD_F64 ? static_cast<float>(static_cast<double>(y[i]) + static_cast<double>(v)) : v;
+  y[i] = mode == LGH_ASSIGN ? v : apply_mode(y[i], v, mode);
 }
 
 template <int WN, int WM, int TN, int TM>

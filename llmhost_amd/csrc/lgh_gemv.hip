@@ -23,6 +23,10 @@ namespace lgh {
 namespace {
 
 
+// Up to three matrices with the same k share one launch and one activation
+// quantization (gemv_q4_pair; the q/k/v projections of an attention block):
+// workgroups [0, wgs0) cover matrix 0, the next wgs1 matrix 1, the rest
+// matrix 2.
 struct Q4GemvArgs {
   const uint8_t *qs0;
   const uint16_t *sc0;
@@ -30,12 +34,17 @@ struct Q4GemvArgs {
   const uint8_t *qs1;
   const uint16_t *sc1;
   float *y1;
+  const uint8_t *qs2;
+  const uint16_t *sc2;
+  float *y2;
   const float *x;
   const int8_t *aq;  // PREQ: ActQ8 codes [k] and scales [k/32] instead of x
   const float *as;
-  int n;
+  const float *nw;   // NORM: rms_norm weight [k]
+  float eps;
+  int n0, n1, n2;    // rows of each matrix
   int bpr;
-  int wgs0;  // workgroups covering matrix 0; the rest cover matrix 1
+  int wgs0, wgs1;
   int mode;
   int per_row;
 };
@@ -44,7 +53,12 @@ struct Q4GemvArgs {
 // PREQ: the activations arrive already quantized (codes + scales, written by
 // the kernel that produced them), so the prologue is two short loads into
 // LDS instead of loading and quantizing x.
-template <int BPL, int KW, int W, bool PREQ>
+// NORM: x is rms_norm'd first (crates/llm-cpu/src/ops.rs:8-23, as
+// rms_norm_kernel): every workgroup holds all of x anyway, so it sums the
+// squares in f64 (DPP tree per wave, then the wave sums in order), takes
+// scale = f32(1 / sqrt(sum * (1/k) + eps)) in f64 and quantizes
+// nw * (x * scale).
+template <int BPL, int KW, int W, bool PREQ, bool NORM = false>
 __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;  // blocks covered by the workgroup (>= bpr)
@@ -57,27 +71,38 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   constexpr int XP = (KB * 4 + THREADS - 1) / THREADS;
   constexpr int XJ = PAIRS ? 2 * XP : (KB * 8 + THREADS - 1) / THREADS;  // float4s of x per thread
   static_assert(W % KW == 0, "slices divide the waves");
+  static_assert(!(PREQ && NORM), "the norm needs x");
   __shared__ __align__(16) int8_t s_qs[KB * 32];
   __shared__ float s_sa[KB];
   __shared__ float s_red[W];
+  __shared__ double s_ss[NORM ? W : 1];
   __shared__ float s_part[KW > 1 ? RG * 4 * KW : 1];
   const int bpr = a.bpr;
   int wg = blockIdx.x;
   const uint8_t *qs = a.qs0;
   const uint16_t *sc = a.sc0;
   float *y = a.y0;
+  int n = a.n0;
   if (wg >= a.wgs0) {
     wg -= a.wgs0;
     qs = a.qs1;
     sc = a.sc1;
     y = a.y1;
+    n = a.n1;
+    if (wg >= a.wgs1) {
+      wg -= a.wgs1;
+      qs = a.qs2;
+      sc = a.sc2;
+      y = a.y2;
+      n = a.n2;
+    }
   }
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = uniform(tid / kWave);
   const int rg = wave / KW, ks = wave % KW;
   const int row0 = (wg * RG + rg) * 4;  // first row of this wave
-  const int rows = uniform(max(0, min(4, a.n - row0)));
+  const int rows = uniform(max(0, min(4, n - row0)));
   const int r = lane >> 4, c = lane & 15;
   const int kb0 = ks * 16 * BPL + c;
 
@@ -86,6 +111,7 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   constexpr int QJ = PREQ ? (KB * 2 + THREADS - 1) / THREADS : 1;
   constexpr int SJ = PREQ ? (KB + THREADS - 1) / THREADS : 1;
   float4 xv[XJ];
+  float4 nv[NORM ? XJ : 1];
   uint4 qv[QJ];
   float sv[SJ];
   if constexpr (PREQ) {
@@ -97,16 +123,24 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     for (int j = 0; j < SJ; j++) sv[j] = buf_load_f32(ar, static_cast<uint32_t>(tid + j * THREADS) * 4u);
   } else {
     const auto xr = make_rsrc(a.x, static_cast<uint32_t>(bpr) * 128u);
+    const auto nr = make_rsrc(a.nw, NORM ? static_cast<uint32_t>(bpr) * 128u : 0u);
     if constexpr (PAIRS) {
 #pragma unroll
       for (int j = 0; j < XP; j++) {
         const uint32_t c = static_cast<uint32_t>(tid + j * THREADS) * 32u;
         xv[2 * j] = buf_load_f4(xr, c);
         xv[2 * j + 1] = buf_load_f4(xr, c + 16u);
+        if constexpr (NORM) {
+          nv[2 * j] = buf_load_f4(nr, c);
+          nv[2 * j + 1] = buf_load_f4(nr, c + 16u);
+        }
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+      for (int j = 0; j < XJ; j++) {
+        xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+        if constexpr (NORM) nv[j] = buf_load_f4(nr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+      }
     }
   }
 
@@ -132,6 +166,34 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
     w[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 16u : kOOB);
     s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
+  }
+
+  // (2b) NORM: normed = nw * (x * scale); elements past k are 0 in x and nw.
+  if constexpr (NORM) {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < XJ; j++) {
+      const double x0 = xv[j].x, x1 = xv[j].y, x2 = xv[j].z, x3 = xv[j].w;
+      ss += x0 * x0;
+      ss += x1 * x1;
+      ss += x2 * x2;
+      ss += x3 * x3;
+    }
+    ss = wave_sum_dpp64(ss);
+    if (lane == 0) s_ss[wave] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < W; i++) tot += s_ss[i];
+    const double inv_dim = 1.0 / static_cast<double>(bpr * 32);
+    const float scale = static_cast<float>(1.0 / sqrt(tot * inv_dim + static_cast<double>(a.eps)));
+#pragma unroll
+    for (int j = 0; j < XJ; j++) {
+      xv[j].x = nv[j].x * (xv[j].x * scale);
+      xv[j].y = nv[j].y * (xv[j].y * scale);
+      xv[j].z = nv[j].z * (xv[j].z * scale);
+      xv[j].w = nv[j].w * (xv[j].w * scale);
+    }
   }
 
   // (3) x -> LDS codes (chunks and scales past the row load as 0).
@@ -184,9 +246,9 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
   }
 }
 
-template <int BPL, int KW, int W, bool PREQ = false>
+template <int BPL, int KW, int W, bool PREQ = false, bool NORM = false>
 hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
-  hipLaunchKernelGGL((q4_gemv_kernel<BPL, KW, W, PREQ>), dim3(total_wgs), dim3(W * kWave), 0, st, a);
+  hipLaunchKernelGGL((q4_gemv_kernel<BPL, KW, W, PREQ, NORM>), dim3(total_wgs), dim3(W * kWave), 0, st, a);
   return hipGetLastError();
 }
 
@@ -694,42 +756,75 @@ hipError_t launch_q4_gemv_codes(const lgh_q4 *w, const int8_t *codes, const floa
 
 hipError_t launch_q4_gemv_any(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                               const int8_t *codes, const float *scales, int mode, int per_row, hipStream_t st) {
-  if (w0->n == 0) return hipSuccess;
-  const int nmat = w1 ? 2 : 1;
-  const Q4GemvPlan p = plan_q4_gemv(w0->n, w0->bpr, nmat);
+  const lgh_q4 *w[2] = {w0, w1};
+  float *y[2] = {y0, y1};
+  return launch_q4_gemv_multi(w, y, w1 ? 2 : 1, x, codes, scales, nullptr, 0.0f, mode, per_row, st);
+}
+
+size_t gemv_multi_rows(const lgh_q4 *const *w, int nmat) {
+  size_t rows = 0;
+  for (int j = 0; j < nmat; j++) rows += w[j]->n;
+  return rows;
+}
+
+hipError_t launch_q4_gemv_multi(const lgh_q4 *const *w, float *const *y, int nmat, const float *x,
+                                const int8_t *codes, const float *scales, const float *norm_w, float eps, int mode,
+                                int per_row, hipStream_t st) {
+  if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
+  const size_t bpr = w[0]->bpr;
+  const size_t rows = gemv_multi_rows(w, nmat);
+  if (rows == 0) return hipSuccess;
+  // The plan depends on the total row count only, as for the pair.
+  const Q4GemvPlan p = plan_q4_gemv(rows, bpr, 1);
   if (!p.ok) return hipErrorInvalidValue;  // K > 16384 * 2: the API uses the GEMM
+  const bool preq = codes != nullptr, norm = norm_w != nullptr;
+  if ((preq && norm) || (norm && p.KW != 1)) return hipErrorInvalidValue;  // the API routes these elsewhere
+  const int rows_per_wg = 4 * p.W / p.KW;
+  int wgs[3] = {0, 0, 0};
   Q4GemvArgs a{};
-  a.qs0 = w0->qs;
-  a.sc0 = w0->sc;
-  a.y0 = y0;
-  a.qs1 = w1 ? w1->qs : nullptr;
-  a.sc1 = w1 ? w1->sc : nullptr;
-  a.y1 = y1;
+  const uint8_t **qsp[3] = {&a.qs0, &a.qs1, &a.qs2};
+  const uint16_t **scp[3] = {&a.sc0, &a.sc1, &a.sc2};
+  float **yp[3] = {&a.y0, &a.y1, &a.y2};
+  int *np[3] = {&a.n0, &a.n1, &a.n2};
+  for (int j = 0; j < nmat; j++) {
+    *qsp[j] = w[j]->qs;
+    *scp[j] = w[j]->sc;
+    *yp[j] = y[j];
+    *np[j] = static_cast<int>(w[j]->n);
+    wgs[j] = static_cast<int>((w[j]->n + rows_per_wg - 1) / rows_per_wg);
+  }
   a.x = x;
   a.aq = codes;
   a.as = scales;
-  a.n = static_cast<int>(w0->n);
-  a.bpr = static_cast<int>(w0->bpr);
-  a.wgs0 = p.wgs_per_mat;
+  a.nw = norm_w;
+  a.eps = eps;
+  a.bpr = static_cast<int>(bpr);
+  a.wgs0 = wgs[0];
+  a.wgs1 = wgs[1];
   a.mode = mode;
   a.per_row = per_row;
-  const int total = p.wgs_per_mat * nmat;
-  const bool preq = codes != nullptr;
+  const int total = wgs[0] + wgs[1] + wgs[2];
+  if (total == 0) return hipSuccess;
 #define LGH_G16(BB, KK, WW)                                                                          \
   if (p.BPL == BB && p.KW == KK && p.W == WW)                                                        \
   return preq ? launch_gemv16<BB, KK, WW, true>(a, total, st) : launch_gemv16<BB, KK, WW, false>(a, total, st)
-  LGH_G16(1, 1, 16);
-  LGH_G16(1, 1, 8);
-  LGH_G16(1, 1, 4);
-  LGH_G16(2, 1, 16);
-  LGH_G16(2, 1, 8);
-  LGH_G16(2, 1, 4);
-  LGH_G16(3, 1, 16);
-  LGH_G16(3, 1, 8);
-  LGH_G16(3, 1, 4);
-  LGH_G16(4, 1, 16);
-  LGH_G16(4, 1, 8);
-  LGH_G16(4, 1, 4);
+#define LGH_G16N(BB, KK, WW)                                                                         \
+  if (p.BPL == BB && p.KW == KK && p.W == WW)                                                        \
+  return preq   ? launch_gemv16<BB, KK, WW, true>(a, total, st)                                     \
+         : norm ? launch_gemv16<BB, KK, WW, false, true>(a, total, st)                              \
+                : launch_gemv16<BB, KK, WW, false>(a, total, st)
+  LGH_G16N(1, 1, 16);
+  LGH_G16N(1, 1, 8);
+  LGH_G16N(1, 1, 4);
+  LGH_G16N(2, 1, 16);
+  LGH_G16N(2, 1, 8);
+  LGH_G16N(2, 1, 4);
+  LGH_G16N(3, 1, 16);
+  LGH_G16N(3, 1, 8);
+  LGH_G16N(3, 1, 4);
+  LGH_G16N(4, 1, 16);
+  LGH_G16N(4, 1, 8);
+  LGH_G16N(4, 1, 4);
   LGH_G16(2, 4, 16);
   LGH_G16(2, 4, 8);
   LGH_G16(2, 4, 4);
@@ -740,6 +835,7 @@ hipError_t launch_q4_gemv_any(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, flo
   LGH_G16(4, 4, 16);
   LGH_G16(4, 8, 16);
 #undef LGH_G16
+#undef LGH_G16N
   return hipErrorInvalidValue;
 }
 

@@ -140,6 +140,14 @@ hipError_t launch_q4_gemv_codes(const lgh_q4 *w, const int8_t *codes, const floa
                                 hipStream_t stream);
 hipError_t launch_q4_gemv_any(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                               const int8_t *codes, const float *scales, int mode, int per_row, hipStream_t stream);
+// Up to three matrices with the same k in one launch sharing x and its
+// quantization (the pair, or an attention block's q/k/v projections), with an
+// optional rms_norm of x in the prologue (norm_w not null; one K slice, i.e.
+// k <= 2048, and x not pre-quantized).  The plan is that of the total rows.
+size_t gemv_multi_rows(const lgh_q4 *const *w, int nmat);
+hipError_t launch_q4_gemv_multi(const lgh_q4 *const *w, float *const *y, int nmat, const float *x,
+                                const int8_t *codes, const float *scales, const float *norm_w, float eps, int mode,
+                                int per_row, hipStream_t stream);
 // Batched GEMV for 2 <= m <= 4 rows of x, quantized inside the kernel
 // (one launch).  ok is false when the shape does not fit.
 struct Q4BatchPlan {

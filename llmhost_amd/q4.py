@@ -381,6 +381,13 @@ def gemm_q4_add(w: Q4Matrix, x, out, m: int) -> None:
     _gemm(w, x, out, m, _ffi.LGH_ADD_F64)
 
 
+def apply_add_inplace(w: Q4Matrix, x, dst, m: int = 1) -> None:
+    """`dst += X @ W^T` in f32, one launch: Linear::apply into a scratch then ops::add_inplace
+    (crates/llm-cpu/src/ops.rs:48-53), the residual step after an attention or conv block's
+    out_proj (crates/llm-engine/src/lfm2.rs:645, 682, 749, 857)."""
+    _gemm(w, x, dst, m, _ffi.LGH_ADD_F32)
+
+
 def gemv_q4_pair(w_gate: Q4Matrix, w_up: Q4Matrix, x, out_gate, out_up) -> None:
     """Gate and up GEMVs sharing one activation quant (gemv_q4.rs:396-443)."""
     ctx = w_gate.ctx
@@ -446,6 +453,36 @@ def ffn_residual(w1: Q4Matrix, w3: Q4Matrix, w2: Q4Matrix, norm_w, eps: float, h
     nw = None if norm_w is None else _np_ptr(_host_f32(norm_w, "norm_w"))
     ctx.check(lib().lgh_q4_ffn_residual(ctx.handle, w1.handle, w3.handle, w2.handle, nw, float(eps),
                                         _np_ptr(hidden), tokens))
+
+
+def norm_gemv(ws, norm_w, eps: float, hidden, outs, tokens: int = 1, mode: int = _ffi.LGH_ASSIGN) -> None:
+    """rms_norm of `tokens` rows of hidden, then outs[j] = W[j] normed for 1..3 matrices with the
+    same K: the q/k/v projections of Lfm2::attn_decode (crates/llm-engine/src/lfm2.rs:784-794) or
+    the in_proj of Lfm2::conv_update (lfm2.rs:651-659).  norm_w None: no norm.  One token with
+    K <= 2048 is one launch sharing one activation quantization; numpy or torch operands."""
+    ws = list(ws)
+    outs = list(outs)
+    _shape_assert(1 <= len(ws) <= 3 and len(outs) == len(ws), "1 to 3 matrices, one output each")
+    ctx = ws[0].ctx
+    k = ws[0].k
+    _shape_assert(all(w.k == k for w in ws), "matrices must share K")
+    handles = (C.c_void_p * len(ws))(*[w.handle.value for w in ws])
+    if _is_torch(hidden):
+        _shape_assert(hidden.numel() == tokens * k, "hidden length != tokens * K")
+        _shape_assert(all(o.numel() == tokens * w.n for o, w in zip(outs, ws)), "out length != tokens * N")
+        ptrs = (C.c_void_p * len(ws))(*[_dev_ptr(o, "out").value for o in outs])
+        nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
+        ctx.check(lib().lgh_q4_norm_gemv_dev(ctx.handle, len(ws), handles, nw, float(eps), _dev_ptr(hidden, "hidden"),
+                                             ptrs, tokens, mode))
+        return
+    hidden = _host_f32(hidden, "hidden")
+    outs = [_host_f32(o, "out") for o in outs]
+    _shape_assert(hidden.size == tokens * k, "hidden length != tokens * K")
+    _shape_assert(all(o.size == tokens * w.n for o, w in zip(outs, ws)), "out length != tokens * N")
+    ptrs = (C.c_void_p * len(ws))(*[o.ctypes.data for o in outs])
+    nw = None if norm_w is None else _np_ptr(_host_f32(norm_w, "norm_w"))
+    ctx.check(lib().lgh_q4_norm_gemv(ctx.handle, len(ws), handles, nw, float(eps), _np_ptr(hidden), ptrs, tokens,
+                                     mode))
 
 
 def ffn_gate_up(w1: Q4Matrix, w3: Q4Matrix, norm_w, eps: float, hidden):
