@@ -13,7 +13,8 @@ weights) + 4*K (x) + 4*N (y) per GEMV.
 Also reported (one JSON line, under "extra"): the 16-layer decode sweep,
 ragged Q4 GEMM M in {4,16,64}, prefill Q4 GEMM M=512 / 2048 TOPS (fraction of
 int8 MFMA peak), Q8_0 GEMV K=N=1536, the tied heads, the decode FFN block
-(fused vs per-op) -- and, on rank 0, the CPU baseline: the
+(fused vs per-op), the attention / conv block input side (norm + projections)
+-- and, on rank 0, the CPU baseline: the
 oracle's runtime-dispatched llm-cpu restatement (VNNI-512 > AVX2 > scalar)
 timed on this host's cores over a bounded sample of the same GEMV workload.
 
@@ -275,6 +276,44 @@ def ffn_case(gb: GpuBench, iters, dim=1536, inter=8192):
             "bytes": byts, "launches": 2}
 
 
+def block_input_case(gb: GpuBench, iters, rows, dim=1536):
+    """Input side of an attention or conv block, one token (lfm2.rs:784-794 / 651-659): rms_norm of
+    hidden, then the block's projections (rows: the matrices' row counts, same K).  The one-launch
+    entry point against the op sequence (rms_norm launch, then one GEMV per matrix).  Rotating
+    weight sets > 2x MALL."""
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    set_bytes = sum(n * (dim // 32) * 18 for n in rows)
+    count = math.ceil(2 * MALL_BYTES / set_bytes)
+    raws = [torch.from_numpy(synth.q4_blocks(700 + j, n, dim).view(np.uint8).copy()).cuda()
+            for j, n in enumerate(rows)]
+    sets = [[q4.Q4Matrix.from_blocks(n, dim, raws[j], gb.ctx) for j, n in enumerate(rows)] for _ in range(count)]
+    del raws
+    hidden = torch.from_numpy(synth.normal_f32(710, dim)).cuda()
+    nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(711, dim)).astype(np.float32)).cuda()
+    normed = torch.zeros(dim, device="cuda")
+    outs = [torch.zeros(n, device="cuda") for n in rows]
+
+    def fused(i):
+        q4.norm_gemv(sets[i % count], nw, 1e-5, hidden, outs)
+
+    def sequence(i):
+        q4.rms_norm(hidden, nw, 1e-5, normed, gb.ctx)
+        for w, o in zip(sets[i % count], outs):
+            q4.gemv_q4(w, normed, o)
+
+    ms_f = gb.timed(fused, iters, 5)
+    ms_s = gb.timed(sequence, iters, 5)
+    for ws in sets:
+        for w in ws:
+            w.free()
+    byts = set_bytes + 8 * dim + 4 * sum(rows)
+    return {"dim": dim, "rows": list(rows), "us": ms_f * 1e3, "gbs": byts / (ms_f * 1e-3) / 1e9,
+            "frac_hbm": byts / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "op_sequence_us": ms_s * 1e3,
+            "bytes": byts, "launches": 1}
+
+
 def cpu_baseline(target_s: float = 12.0):
     """The oracle's llm-cpu restatement (runtime-dispatched kernel, pinned
     pool) on this host, over rotating packed copies larger than the LLC."""
@@ -434,6 +473,9 @@ def main():
                            (1536, 8192), (4096, 8192), (16384, 8192))]
         log("[bench] decode FFN block (fused vs per-op)")
         extra["ffn_block_dim1536_inter8192"] = ffn_case(gb, 100)
+        log("[bench] attention / conv block input side (norm + projections, fused vs op sequence)")
+        extra["attn_qkv_dim1536"] = block_input_case(gb, 100, (1536, 512, 512))
+        extra["conv_in_proj_dim1536"] = block_input_case(gb, 100, (4608,))
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")
