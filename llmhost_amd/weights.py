@@ -87,6 +87,20 @@ def apply_pair(w1: Linear, w3: Linear, x, tokens: int, out1, out3) -> None:
         w3.apply(x, tokens, out3)
 
 
+def norm_then_apply(linears, norm_w, eps: float, hidden, tokens: int, outs) -> None:
+    """`normed = rms_norm(hidden)` then `linears[j].apply(normed, tokens, outs[j])` for 1..3 Q4
+    linears sharing K: Lfm2::attn_decode's q/k/v (lfm2.rs:784-794) and conv_update's in_proj
+    (lfm2.rs:651-659).  norm_w None: no norm.  One launch for a decode token with K <= 2048."""
+    _q4.norm_gemv([lin.mat for lin in linears], norm_w, eps, hidden, outs, tokens)
+
+
+def apply_then_add_inplace(linear: Linear, x, tokens: int, hidden) -> None:
+    """`projected = linear.apply(x)` then `add_inplace(hidden, projected)` (ops.rs:48-53;
+    lfm2.rs:645, 682, 749, 857): hidden += W x in f32, in one launch."""
+    linear._check(x, tokens, hidden)
+    _q4.apply_add_inplace(linear.mat, x, hidden, tokens)
+
+
 class OutputHead:
     """Tied LM head, Q4 Linear or Q8_0 (weights.rs:156-192)."""
 

@@ -147,3 +147,27 @@ def test_add_f32_mode_codes_gemv(gpu_ctx):
     got = y0.copy()
     q4._gemv_prep(w, acts, got, LGH_ADD_F32)
     assert np.array_equal(got.view(np.uint32), (y0 + assign).view(np.uint32))
+
+
+def test_seam_mirror_block_sides(gpu_ctx, oracle):
+    """weights.norm_then_apply / apply_then_add_inplace on Linear objects (the seam mirror)."""
+    from llmhost_amd import weights
+
+    k, rows = 256, (256, 64, 64)
+    gw, cw = _mats(gpu_ctx, oracle, k, rows, 950)
+    lins = [weights.Linear(w) for w in gw]
+    hidden, nw = _hidden(k, 1, 951)
+    outs = [np.zeros(n, dtype=np.float32) for n in rows]
+    weights.norm_then_apply(lins, nw, EPS, hidden, 1, outs)
+    normed = oracle.rms_norm(hidden, nw, EPS)
+    for o, c in zip(outs, cw):
+        assert_close(o, oracle.gemv_q4(c, normed, kernel=oracle.KERNEL_SCALAR), what="q/k/v")
+    # out_proj (256 x 64 here: the v rows back to hidden) + f32 residual
+    wo = weights.Linear(gw[0])
+    h2 = hidden.copy()
+    weights.apply_then_add_inplace(wo, outs[0], 1, h2)
+    proj = np.zeros(256, dtype=np.float32)
+    wo.apply(outs[0], 1, proj)
+    assert np.array_equal(h2.view(np.uint32), (hidden + proj).view(np.uint32))
+    with pytest.raises(LghShapeError):
+        weights.apply_then_add_inplace(wo, outs[1], 1, h2)
