@@ -312,6 +312,38 @@ __device__ __forceinline__ uint2 act_quant_group4(float4 a, float4 b, bool per_r
                     __builtin_amdgcn_perm(q[5], q[4], 0x0c0c0400u) | __builtin_amdgcn_perm(q[7], q[6], 0x04000c0cu));
 }
 
+// ---- rms_norm scale ------------------------------------------------------------
+// scale = f32(1 / sqrt(sumsq * inv_dim + eps)) with the reference's roundings
+// (crates/llm-cpu/src/ops.rs:12-17: f64 multiply, f64 add, f64 sqrt, f64
+// reciprocal, then `as f32`).  The multiply and add are rounded separately
+// (no contraction into an FMA).  1/sqrt(v) comes from v_rsq_f64 refined by
+// two Newton steps: r lies within a few f64 ulp of the true value, as does the
+// reference's RN64(1 / RN64(sqrt v)), so both round to the same f32 unless an
+// f32 rounding boundary lies within 2^-40 of r (relative); then, and for v
+// outside [2^-1000, 2^1000], the IEEE sqrt and division decide, on a real
+// (wave-uniform) branch.
+__device__ __forceinline__ float rms_scale(double sumsq, double inv_dim, float eps) {
+  const double v = __dadd_rn(__dmul_rn(sumsq, inv_dim), static_cast<double>(eps));
+  if (v > 0x1p-1000 && v < 0x1p1000) {
+    double y = __builtin_amdgcn_rsq(v);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const double e = __builtin_fma(-v, y * y, 1.0);
+      y = __builtin_fma(0.5 * y, e, y);
+    }
+    const float f = static_cast<float>(y);
+    const uint32_t fb = __builtin_bit_cast(uint32_t, f);
+    const double fd = f;
+    const double up = 0.5 * (fd + static_cast<double>(__builtin_bit_cast(float, fb + 1u)));
+    const double dn = 0.5 * (fd + static_cast<double>(__builtin_bit_cast(float, fb - 1u)));
+    const double tol = y * 0x1p-40;
+    if (fb > 1u && fb < 0x7F7FFFFFu && __builtin_fabs(y - up) > tol && __builtin_fabs(y - dn) > tol) return f;
+  }
+  double t = v;
+  asm volatile("" : "+v"(t));  // keep the exact path behind the branch
+  return static_cast<float>(1.0 / __builtin_sqrt(t));
+}
+
 // ---- x -> LDS codes, shared by the GEMV-style kernels --------------------
 // Quantize the float4s held in registers (thread t holds x4[t + THREADS j])
 // into LDS: s_qs (natural order) and s_sa, for blocks [0, nblk).  All

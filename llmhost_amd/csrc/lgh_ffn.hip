@@ -30,6 +30,7 @@ struct FfnUpArgs {
   const uint16_t *sc1, *sc3;
   const float *x;   // hidden [k]
   const float *nw;  // norm weight [k], or null for no norm
+  double inv_k;     // 1 / k in f64 (ops.rs:12)
   float eps;
   int bpr;        // k / 32
   int per_row;    // ActQ8 mode for `normed`
@@ -104,8 +105,7 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
     double tot = 0.0;
 #pragma unroll
     for (int i = 0; i < kFfnWaves; i++) tot += s_ss[i];
-    const double inv_dim = 1.0 / static_cast<double>(bpr * 32);
-    const float scale = static_cast<float>(1.0 / sqrt(tot * inv_dim + static_cast<double>(a.eps)));
+    const float scale = rms_scale(tot, a.inv_k, a.eps);
 #pragma unroll
     for (int j = 0; j < XJ; j++) {
       xv[j].x = nv[j].x * (xv[j].x * scale);
@@ -165,8 +165,8 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
 constexpr int kNormThreads = 256;
 
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *__restrict__ x,
-                                                                const float *__restrict__ w, int dim, float eps,
-                                                                float *__restrict__ out) {
+                                                                const float *__restrict__ w, int dim, double inv_dim,
+                                                                float eps, float *__restrict__ out) {
   __shared__ double s_ss[kNormThreads / kWave];
   const float *row = x + static_cast<size_t>(blockIdx.x) * dim;
   float *dst = out + static_cast<size_t>(blockIdx.x) * dim;
@@ -181,8 +181,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *__r
   double tot = 0.0;
 #pragma unroll
   for (int i = 0; i < kNormThreads / kWave; i++) tot += s_ss[i];
-  const double inv_dim = 1.0 / static_cast<double>(dim);
-  const float scale = static_cast<float>(1.0 / sqrt(tot * inv_dim + static_cast<double>(eps)));
+  const float scale = rms_scale(tot, inv_dim, eps);
   for (int i = threadIdx.x; i < dim; i += kNormThreads) dst[i] = w[i] * (row[i] * scale);
 }
 
@@ -210,8 +209,8 @@ hipError_t launch_ffn_gate_up(const lgh_q4 *w1, const lgh_q4 *w3, const float *x
                               hipStream_t st) {
   if (!ffn_gate_up_supported(w1)) return hipErrorInvalidValue;
   if (w1->n == 0) return hipSuccess;
-  const FfnUpArgs a{w1->qs, w3->qs, w1->sc, w3->sc, x, norm_w, eps, static_cast<int>(w1->bpr), per_row,
-                    hq, hs, hf, g, u};
+  const FfnUpArgs a{w1->qs, w3->qs, w1->sc, w3->sc, x, norm_w, 1.0 / static_cast<double>(w1->k), eps,
+                    static_cast<int>(w1->bpr), per_row, hq, hs, hf, g, u};
   const int wgs = static_cast<int>(w1->n / 32);
   switch ((w1->bpr + 15) / 16) {
     case 1: return launch_gate_up<1>(a, wgs, st);
@@ -225,7 +224,7 @@ hipError_t launch_rms_norm(const float *x, const float *w, size_t dim, size_t ro
                            hipStream_t st) {
   if (rows == 0 || dim == 0) return hipSuccess;
   hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, st, x, w,
-                     static_cast<int>(dim), eps, out);
+                     static_cast<int>(dim), 1.0 / static_cast<double>(dim), eps, out);
   return hipGetLastError();
 }
 

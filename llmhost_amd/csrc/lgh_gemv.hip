@@ -41,6 +41,7 @@ struct Q4GemvArgs {
   const int8_t *aq;  // PREQ: ActQ8 codes [k] and scales [k/32] instead of x
   const float *as;
   const float *nw;   // NORM: rms_norm weight [k]
+  double inv_k;      // NORM: 1 / k in f64, as the reference computes it (ops.rs:12)
   float eps;
   int n0, n1, n2;    // rows of each matrix
   int bpr;
@@ -185,8 +186,7 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     double tot = 0.0;
 #pragma unroll
     for (int i = 0; i < W; i++) tot += s_ss[i];
-    const double inv_dim = 1.0 / static_cast<double>(bpr * 32);
-    const float scale = static_cast<float>(1.0 / sqrt(tot * inv_dim + static_cast<double>(a.eps)));
+    const float scale = rms_scale(tot, a.inv_k, a.eps);
 #pragma unroll
     for (int j = 0; j < XJ; j++) {
       xv[j].x = nv[j].x * (xv[j].x * scale);
@@ -797,6 +797,7 @@ hipError_t launch_q4_gemv_multi(const lgh_q4 *const *w, float *const *y, int nma
   a.aq = codes;
   a.as = scales;
   a.nw = norm_w;
+  a.inv_k = 1.0 / static_cast<double>(bpr * 32);
   a.eps = eps;
   a.bpr = static_cast<int>(bpr);
   a.wgs0 = wgs[0];
