@@ -312,6 +312,11 @@ __device__ __forceinline__ uint2 act_quant_group4(float4 a, float4 b, bool per_r
                     __builtin_amdgcn_perm(q[5], q[4], 0x0c0c0400u) | __builtin_amdgcn_perm(q[7], q[6], 0x04000c0cu));
 }
 
+// silu(g) * u in f32 (crates/llm-cpu/src/ops.rs:27-36 silu, then the gate
+// multiply, crates/llm-engine/src/lfm2.rs:902-905) -- one definition, so every
+// kernel that forms h rounds it identically.
+__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
 // ---- rms_norm scale ------------------------------------------------------------
 // scale = f32(1 / sqrt(sumsq * inv_dim + eps)) with the reference's roundings
 // (crates/llm-cpu/src/ops.rs:12-17: f64 multiply, f64 add, f64 sqrt, f64

@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
   if (wave == 0) {
     if (lane < 32) {
       const float g = s_gu[0][lane], u = s_gu[1][lane];
-      const float h = (g / (1.0f + expf(-g))) * u;
+      const float h = silu_mul1(g, u);
       s_h[lane] = h;
       if (a.g_out) a.g_out[base + lane] = g;
       if (a.u_out) a.u_out[base + lane] = u;
@@ -190,8 +190,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ g, co
                                                        size_t n) {
   const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n) return;
-  const float x = g[i];
-  g[i] = (x / (1.0f + expf(-x))) * u[i];
+  g[i] = silu_mul1(g[i], u[i]);
 }
 
 template <int BPL>
