@@ -276,11 +276,12 @@ def ffn_case(gb: GpuBench, iters, dim=1536, inter=8192):
             "bytes": byts, "launches": 2}
 
 
-def block_input_case(gb: GpuBench, iters, rows, dim=1536):
-    """Input side of an attention or conv block, one token (lfm2.rs:784-794 / 651-659): rms_norm of
-    hidden, then the block's projections (rows: the matrices' row counts, same K).  The one-launch
-    entry point against the op sequence (rms_norm launch, then one GEMV per matrix).  Rotating
-    weight sets > 2x MALL."""
+def block_input_case(gb: GpuBench, iters, rows, dim=1536, tokens=1):
+    """Input side of an attention or conv block (lfm2.rs:784-794 / 651-659; prefill 698-711):
+    rms_norm of `tokens` rows of hidden, then the block's projections (rows: the matrices' row
+    counts, same K).  The entry point (one launch for a decode token; for several tokens one
+    activation quantization shared by the matrices) against the op sequence (rms_norm, then one
+    GEMV / GEMM per matrix).  Rotating weight sets > 2x MALL."""
     torch, q4 = gb.torch, gb.q4
     from llmhost_amd import synth
 
@@ -290,28 +291,29 @@ def block_input_case(gb: GpuBench, iters, rows, dim=1536):
             for j, n in enumerate(rows)]
     sets = [[q4.Q4Matrix.from_blocks(n, dim, raws[j], gb.ctx) for j, n in enumerate(rows)] for _ in range(count)]
     del raws
-    hidden = torch.from_numpy(synth.normal_f32(710, dim)).cuda()
+    hidden = torch.from_numpy(synth.normal_f32(710, tokens * dim)).cuda()
     nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(711, dim)).astype(np.float32)).cuda()
-    normed = torch.zeros(dim, device="cuda")
-    outs = [torch.zeros(n, device="cuda") for n in rows]
+    normed = torch.zeros(tokens * dim, device="cuda")
+    outs = [torch.zeros(tokens * n, device="cuda") for n in rows]
 
     def fused(i):
-        q4.norm_gemv(sets[i % count], nw, 1e-5, hidden, outs)
+        q4.norm_gemv(sets[i % count], nw, 1e-5, hidden, outs, tokens)
 
     def sequence(i):
         q4.rms_norm(hidden, nw, 1e-5, normed, gb.ctx)
         for w, o in zip(sets[i % count], outs):
-            q4.gemv_q4(w, normed, o)
+            q4.gemm_q4(w, normed, o, tokens)
 
     ms_f = gb.timed(fused, iters, 5)
     ms_s = gb.timed(sequence, iters, 5)
     for ws in sets:
         for w in ws:
             w.free()
-    byts = set_bytes + 8 * dim + 4 * sum(rows)
-    return {"dim": dim, "rows": list(rows), "us": ms_f * 1e3, "gbs": byts / (ms_f * 1e-3) / 1e9,
-            "frac_hbm": byts / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "op_sequence_us": ms_s * 1e3,
-            "bytes": byts, "launches": 1}
+    byts = set_bytes + 4 * dim * (tokens + 1) + 4 * tokens * sum(rows)
+    ops = 2.0 * tokens * dim * sum(rows)
+    return {"dim": dim, "rows": list(rows), "tokens": tokens, "us": ms_f * 1e3,
+            "gbs": byts / (ms_f * 1e-3) / 1e9, "frac_hbm": byts / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "tops": ops / (ms_f * 1e-3) / 1e12, "op_sequence_us": ms_s * 1e3, "bytes": byts}
 
 
 def cpu_baseline(target_s: float = 12.0):
@@ -476,6 +478,7 @@ def main():
         log("[bench] attention / conv block input side (norm + projections, fused vs op sequence)")
         extra["attn_qkv_dim1536"] = block_input_case(gb, 100, (1536, 512, 512))
         extra["conv_in_proj_dim1536"] = block_input_case(gb, 100, (4608,))
+        extra["attn_qkv_dim1536_prefill_m512"] = block_input_case(gb, 10, (1536, 512, 512), tokens=512)
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")

@@ -477,23 +477,32 @@ int lgh_act_quant_dev(lgh_ctx *ctx, const float *x_dev, size_t m, size_t k, int8
   return LGH_OK;
 }
 
-int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
-  if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
-  if (int r = check_mode(ctx, mode)) return r;
-  if (m == 0 || w->n == 0) return LGH_OK;
-  if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+// y[j] = x @ W[j]^T for 1..3 matrices with the same k, m rows of x: the
+// activation quantization of each route (the MMA image, the GEMM's operand
+// image) is done once and read by every matrix.  m == 1 and m <= 4 quantize
+// inside their kernels, per matrix.
+static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const float *x_dev, float *const *y_dev,
+                          size_t m, int mode) {
+  const size_t k = w[0]->k, bpr = w[0]->bpr;
+  size_t nmax = 0;
+  for (int j = 0; j < nmat; j++) nmax = std::max(nmax, w[j]->n);
+  if (m == 0 || nmax == 0) return LGH_OK;
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  if (m == 1 && lgh::plan_q4_gemv(w->n, w->bpr, 1).ok) return lgh_q4_gemv_dev(ctx, w, x_dev, y_dev, mode);
-  // Small batches are weight-stream bound: nibble planes, no operand image.
-  if (lgh::plan_q4_batch(m, w->bpr).ok) {  // m <= 4: x quantized inside the kernel, dot4
-    if (int r = set_device(ctx)) return r;
-    LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w, x_dev, y_dev, m, mode, ctx->act_mode, ctx->stream));
+  if (m == 1 && lgh::plan_q4_gemv(nmax, bpr, 1).ok) {
+    for (int j = 0; j < nmat; j++)
+      if (w[j]->n)
+        if (int r = launch_gemv(ctx, w[j], y_dev[j], nullptr, nullptr, x_dev, mode)) return r;
     return LGH_OK;
   }
-  if (lgh::plan_q4_mma(w->n, m, w->bpr).ok) {  // m <= 64: activation image, then int8 MFMA per block
-    if (int r = set_device(ctx)) return r;
-    const size_t mt = (m + 15) / 16, pq = (w->bpr + 3) / 4;
+  if (int r = set_device(ctx)) return r;
+  // Small batches are weight-stream bound: nibble planes, no operand image.
+  if (lgh::plan_q4_batch(m, bpr).ok) {  // m <= 4: x quantized inside the kernel, dot4
+    for (int j = 0; j < nmat; j++)
+      LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w[j], x_dev, y_dev[j], m, mode, ctx->act_mode, ctx->stream));
+    return LGH_OK;
+  }
+  if (lgh::plan_q4_mma(nmax, m, bpr).ok) {  // m <= 64: activation image, then int8 MFMA per block
+    const size_t mt = (m + 15) / 16, pq = (bpr + 3) / 4;
     Carve cv;
     const size_t o_ci = cv.take(mt * pq * 2 * 1024), o_si = cv.take(mt * pq * 256);
     const size_t o_rs = cv.take(m * sizeof(float));
@@ -501,23 +510,30 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
     char *ws = static_cast<char *>(ctx->ws);
     auto *ci = reinterpret_cast<uint8_t *>(ws + o_ci);
     auto *si = reinterpret_cast<float *>(ws + o_si);
-    LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev, m, w->k, ctx->act_mode, ci, si,
+    LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev, m, k, ctx->act_mode, ci, si,
                                            reinterpret_cast<float *>(ws + o_rs), ctx->stream));
-    LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w, ci, si, y_dev, m, mode, ctx->stream));
+    for (int j = 0; j < nmat; j++)
+      if (w[j]->n) LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w[j], ci, si, y_dev[j], m, mode, ctx->stream));
     return LGH_OK;
   }
-  if (!w->mx) return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w->n, w->k);
-  if (int r = set_device(ctx)) return r;
+  for (int j = 0; j < nmat; j++)
+    if (w[j]->n && !w[j]->mx)
+      return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w[j]->n, w[j]->k);
   // Tokens per launch: the activation image must fit 31-bit buffer offsets.
-  const size_t rec_per_tile = w->pp * lgh::kMxARec;
+  const size_t pp = (bpr + 1) / 2;
+  const size_t rec_per_tile = pp * lgh::kMxARec;
   const size_t cap_tiles = lgh::kMxMaxBytes / rec_per_tile;
-  if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", w->k);
+  if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", k);
   const size_t chunk = std::min(m, (cap_tiles - 8) * 32);
-  const int splits = lgh::plan_q4_gemm_splits(w, chunk);
+  size_t part_floats = 0;
+  for (int j = 0; j < nmat; j++) {
+    if (!w[j]->n) continue;
+    const int splits = lgh::plan_q4_gemm_splits(w[j], chunk);
+    if (splits > 1) part_floats = std::max(part_floats, static_cast<size_t>(splits) * chunk * w[j]->n);
+  }
   Carve cv;
   const size_t o_mx = cv.take((chunk + 31) / 32 * rec_per_tile);
   const size_t o_rs = cv.take(chunk * sizeof(float));
-  const size_t part_floats = splits > 1 ? splits * chunk * w->n : 0;
   const size_t o_part = cv.take(part_floats * sizeof(float));
   if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
   char *ws = static_cast<char *>(ctx->ws);
@@ -526,10 +542,24 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   auto *part = reinterpret_cast<float *>(ws + o_part);
   for (size_t m0 = 0; m0 < m; m0 += chunk) {
     const size_t mc = std::min(chunk, m - m0);
-    LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * w->k, mc, w->k, ctx->act_mode, mxa, rs, ctx->stream));
-    LGH_HIP(ctx, lgh::launch_q4_gemm(w, mxa, y_dev + m0 * w->n, mc, mode, part, part_floats, ctx->stream));
+    LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * k, mc, k, ctx->act_mode, mxa, rs, ctx->stream));
+    for (int j = 0; j < nmat; j++)
+      if (w[j]->n)
+        LGH_HIP(ctx, lgh::launch_q4_gemm(w[j], mxa, y_dev[j] + m0 * w[j]->n, mc, mode, part, part_floats,
+                                         ctx->stream));
   }
   return LGH_OK;
+}
+
+int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (m == 0 || w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  const lgh_q4 *ws[1] = {w};
+  float *ys[1] = {y_dev};
+  return gemm_multi_dev(ctx, ws, 1, x_dev, ys, m, mode);
 }
 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev, size_t tokens) {
@@ -708,8 +738,9 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
   float *normed = norm_w_dev ? reinterpret_cast<float *>(f + o_n) : hidden_dev;
   float *g = reinterpret_cast<float *>(f + o_g), *u = reinterpret_cast<float *>(f + o_u);
   if (norm_w_dev) LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, dim, tokens, eps, normed, ctx->stream));
-  if (int r = lgh_q4_gemm_dev(ctx, w1, normed, g, tokens, LGH_ASSIGN)) return r;
-  if (int r = lgh_q4_gemm_dev(ctx, w3, normed, u, tokens, LGH_ASSIGN)) return r;
+  const lgh_q4 *gate_up[2] = {w1, w3};
+  float *gu[2] = {g, u};
+  if (int r = gemm_multi_dev(ctx, gate_up, 2, normed, gu, tokens, LGH_ASSIGN)) return r;
   LGH_HIP(ctx, lgh::launch_silu_mul(g, u, tokens * inter, ctx->stream));
   return lgh_q4_gemm_dev(ctx, w2, g, hidden_dev, tokens, LGH_ADD_F64);
 }
@@ -802,7 +833,8 @@ int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, cons
                                            ctx->act_mode, ctx->stream));
     return LGH_OK;
   }
-  // Otherwise the reference's sequence (rms_norm, then one apply per matrix).
+  // Otherwise the reference's sequence (rms_norm, then one apply per matrix;
+  // the matrices share each route's activation quantization).
   const float *normed = hidden_dev;
   if (norm_w_dev && k) {
     if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, tokens * k * sizeof(float))) return r;
@@ -810,9 +842,7 @@ int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, cons
     LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, k, tokens, eps, nd, ctx->stream));
     normed = nd;
   }
-  for (size_t j = 0; j < nmat; j++)
-    if (int r = lgh_q4_gemm_dev(ctx, w[j], normed, y_dev[j], tokens, mode)) return r;
-  return LGH_OK;
+  return gemm_multi_dev(ctx, w, nm, normed, y_dev, tokens, mode);
 }
 
 int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,
