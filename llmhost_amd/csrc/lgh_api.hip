@@ -525,12 +525,10 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
   const size_t cap_tiles = lgh::kMxMaxBytes / rec_per_tile;
   if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", k);
   const size_t chunk = std::min(m, (cap_tiles - 8) * 32);
-  size_t part_floats = 0;
-  for (int j = 0; j < nmat; j++) {
-    if (!w[j]->n) continue;
-    const int splits = lgh::plan_q4_gemm_splits(w[j], chunk);
-    if (splits > 1) part_floats = std::max(part_floats, static_cast<size_t>(splits) * chunk * w[j]->n);
-  }
+  size_t rows = 0;
+  for (int j = 0; j < nmat; j++) rows += w[j]->n;
+  const int splits = lgh::plan_q4_gemm_splits(w, nmat, chunk);
+  const size_t part_floats = splits > 1 ? static_cast<size_t>(splits) * chunk * rows : 0;
   Carve cv;
   const size_t o_mx = cv.take((chunk + 31) / 32 * rec_per_tile);
   const size_t o_rs = cv.take(chunk * sizeof(float));
@@ -542,11 +540,10 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
   auto *part = reinterpret_cast<float *>(ws + o_part);
   for (size_t m0 = 0; m0 < m; m0 += chunk) {
     const size_t mc = std::min(chunk, m - m0);
+    float *yc[3] = {nullptr, nullptr, nullptr};
+    for (int j = 0; j < nmat; j++) yc[j] = w[j]->n ? y_dev[j] + m0 * w[j]->n : nullptr;
     LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * k, mc, k, ctx->act_mode, mxa, rs, ctx->stream));
-    for (int j = 0; j < nmat; j++)
-      if (w[j]->n)
-        LGH_HIP(ctx, lgh::launch_q4_gemm(w[j], mxa, y_dev[j] + m0 * w[j]->n, mc, mode, part, part_floats,
-                                         ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemm(w, nmat, mxa, yc, mc, mode, part, part_floats, ctx->stream));
   }
   return LGH_OK;
 }

@@ -46,6 +46,14 @@ struct GemmArgs {
   uint32_t w_bytes, a_bytes;
 };
 
+// Up to three matrices with the same k on the same activation image in one
+// launch (the q / k / v or gate / up projections of one input): grid.x runs
+// over the N tiles of matrix 0, then of matrix 1, then of matrix 2.
+struct GemmMulti {
+  GemmArgs g[3];
+  int gx0, gx1;  // N-tile groups of matrices 0 and 1
+};
+
 template <int WN, int WM, int TN, int TM>
 struct Cfg {
   static constexpr int NS = WN * TN;  // 32-row weight tiles per workgroup
@@ -235,7 +243,7 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> 
 }
 
 template <int WN, int WM, int TN, int TM>
-__global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmMulti gm) {
   using C = Cfg<WN, WM, TN, TM>;
   // Three stage buffers as distinct objects, so the compiler can tell the
   // buffer being read from the ones the DMA is filling.
@@ -246,7 +254,17 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmArgs g) {
   const int wave = uniform(threadIdx.x >> 6);
   const int wn = wave % WN, wm = wave / WN;
   const int row = lane & 31, half = lane >> 5;
-  const int nt0 = blockIdx.x * C::NS, mt0 = blockIdx.y * C::MS;
+  int bx = blockIdx.x, mat = 0;
+  if (bx >= gm.gx0) {
+    bx -= gm.gx0;
+    mat = 1;
+    if (bx >= gm.gx1) {
+      bx -= gm.gx1;
+      mat = 2;
+    }
+  }
+  const GemmArgs &g = gm.g[uniform(mat)];
+  const int nt0 = bx * C::NS, mt0 = blockIdx.y * C::MS;
 
   float acc[TN][TM][16];
 #pragma unroll
@@ -338,14 +356,44 @@ __global__ __launch_bounds__(64) void q4_mx_block_dots_kernel(const uint8_t *__r
   }
 }
 
-// y = sum over splits of part[z] (z ascending), then the caller's mode.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int splits,
-                                                            size_t total, float *y, int mode) {
-  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  float v = part[i];
-  for (int z = 1; z < splits; z++) v += part[static_cast<size_t>(z) * total + i];
-  y[i] = mode == LGH_ASSIGN ? v : apply_mode(y[i], v, mode);
+// y = sum over splits of part[z] (z ascending), then the caller's mode, for
+// the outputs of a launch over up to three matrices: element i of their
+// concatenation belongs to matrix j = the first with i < end[j].
+struct ReduceMulti {
+  const float *part[3];
+  float *y[3];
+  size_t end[3];  // cumulative m * n
+  int splits, mode;
+};
+
+__global__ __launch_bounds__(256) void splitk_reduce_multi_kernel(ReduceMulti r) {
+  size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= r.end[2]) return;
+  int j = 0;
+  size_t begin = 0;
+  if (i >= r.end[0]) {
+    j = 1;
+    begin = r.end[0];
+    if (i >= r.end[1]) {
+      j = 2;
+      begin = r.end[1];
+    }
+  }
+  const size_t total = r.end[j] - begin, e = i - begin;
+  const float *part = r.part[j];
+  float v = part[e];
+  for (int z = 1; z < r.splits; z++) v += part[static_cast<size_t>(z) * total + e];
+  float *y = r.y[j];
+  y[e] = r.mode == LGH_ASSIGN ? v : apply_mode(y[e], v, r.mode);
+}
+
+template <int WN, int WM, int TN, int TM>
+int splits_for_tiles(long tiles, size_t pp) {
+  // Split K when the tiles alone leave CUs idle: aim for >= kSplitTarget
+  // workgroups while keeping >= 8 block pairs per split.
+  int splits = 1;
+  while (tiles * splits < kSplitTarget && pp / (2 * splits) >= 8) splits *= 2;
+  return splits;
 }
 
 template <int WN, int WM, int TN, int TM>
@@ -360,17 +408,33 @@ int splits_for(size_t nt, size_t mt, size_t pp) {
 }
 
 template <int WN, int WM, int TN, int TM>
-hipError_t launch_cfg(GemmArgs g, int splits, float *part, hipStream_t st) {
+hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
   using C = Cfg<WN, WM, TN, TM>;
-  const size_t mn = static_cast<size_t>(g.m) * g.n;
-  g.splits = splits;
-  g.part = part;
-  const dim3 grid((g.nt + C::NS - 1) / C::NS, (g.mt + C::MS - 1) / C::MS, splits);
-  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), 0, st, g);
+  int gx[3] = {0, 0, 0};
+  for (int j = 0; j < nmat; j++) {
+    gm.g[j].splits = splits;
+    gx[j] = (gm.g[j].nt + C::NS - 1) / C::NS;
+  }
+  gm.gx0 = gx[0];
+  gm.gx1 = gx[1];
+  const dim3 grid(static_cast<unsigned>(gx[0] + gx[1] + gx[2]), (gm.g[0].mt + C::MS - 1) / C::MS, splits);
+  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), 0, st, gm);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, st, part,
-                     splits, mn, g.y, g.mode);
+  ReduceMulti r{};
+  size_t end = 0;
+  for (int j = 0; j < 3; j++) {
+    if (j < nmat) {
+      r.part[j] = gm.g[j].part;
+      r.y[j] = gm.g[j].y;
+      end += static_cast<size_t>(gm.g[j].m) * gm.g[j].n;
+    }
+    r.end[j] = end;
+  }
+  r.splits = splits;
+  r.mode = gm.g[0].mode;
+  hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3(static_cast<unsigned>((end + 255) / 256)), dim3(256), 0, st,
+                     r);
   return hipGetLastError();
 }
 
@@ -381,29 +445,43 @@ hipError_t launch_cfg(GemmArgs g, int splits, float *part, hipStream_t st) {
 // fast as or faster than 128 x 64 and 128 x 128 -- the inner loop is bound by
 // the matrix core plus the fold (which do not overlap on gfx950), and the
 // small tile keeps the most workgroups resident to cover the stage loads.
-int plan_q4_gemm_splits(const lgh_q4 *w, size_t m) { return splits_for<4, 1, 1, 1>(w->nt, (m + 31) / 32, w->pp); }
+int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m) {
+  using C = Cfg<4, 1, 1, 1>;
+  long tiles = 0;
+  for (int j = 0; j < nmat; j++) tiles += static_cast<long>((w[j]->nt + C::NS - 1) / C::NS);
+  tiles *= static_cast<long>(((m + 31) / 32 + C::MS - 1) / C::MS);
+  return splits_for_tiles<4, 1, 1, 1>(tiles, w[0]->pp);
+}
 
-hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t m, int mode, float *part,
-                          size_t part_floats, hipStream_t st) {
-  if (w->n == 0 || m == 0) return hipSuccess;
-  int splits = plan_q4_gemm_splits(w, m);
-  while (splits > 1 && static_cast<size_t>(splits) * m * w->n > part_floats) splits /= 2;
+hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
+                          float *part, size_t part_floats, hipStream_t st) {
+  if (m == 0 || nmat < 1 || nmat > 3) return m == 0 ? hipSuccess : hipErrorInvalidValue;
+  size_t rows = 0;
+  for (int j = 0; j < nmat; j++) rows += w[j]->n;
+  if (rows == 0) return hipSuccess;
+  int splits = plan_q4_gemm_splits(w, nmat, m);
+  while (splits > 1 && static_cast<size_t>(splits) * m * rows > part_floats) splits /= 2;
   const size_t mt = (m + 31) / 32;
-  GemmArgs g{w->mx,
-             mxa,
-             y,
-             nullptr,
-             static_cast<int>(w->n),
-             static_cast<int>(m),
-             static_cast<int>(w->nt),
-             static_cast<int>(mt),
-             static_cast<int>(w->pp),
-             mode,
-             (w->n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0) ? 1 : 0,
-             1,
-             static_cast<uint32_t>(w->nt * w->pp * kMxWRec),
-             static_cast<uint32_t>(mt * w->pp * kMxARec)};
-  return launch_cfg<4, 1, 1, 1>(g, splits, part, st);
+  GemmMulti gm{};
+  size_t off = 0;
+  for (int j = 0; j < nmat; j++) {
+    gm.g[j] = GemmArgs{w[j]->mx,
+                       mxa,
+                       y[j],
+                       splits > 1 ? part + static_cast<size_t>(splits) * m * off : nullptr,
+                       static_cast<int>(w[j]->n),
+                       static_cast<int>(m),
+                       static_cast<int>(w[j]->nt),
+                       static_cast<int>(mt),
+                       static_cast<int>(w[j]->pp),
+                       mode,
+                       (w[j]->n % 4 == 0 && (reinterpret_cast<uintptr_t>(y[j]) & 15u) == 0) ? 1 : 0,
+                       1,
+                       static_cast<uint32_t>(w[j]->nt * w[j]->pp * kMxWRec),
+                       static_cast<uint32_t>(mt * w[j]->pp * kMxARec)};
+    off += w[j]->n;
+  }
+  return launch_cfg<4, 1, 1, 1>(gm, nmat, splits, st);
 }
 
 hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const uint8_t *mxa, size_t m, int32_t *out,

@@ -185,13 +185,15 @@ hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t toke
 hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int8_t *qs,
                             float *scales, int32_t *sums, float *row_scale, hipStream_t stream);
 
-// GEMM on an activation operand image: y[m][n] (+)= x[m][k] . W^T.
-// plan_q4_gemm_splits() is the number of K splits the launch wants for m
-// tokens; `part` holds part_floats floats of scratch, and the launch uses
-// fewer splits when splits * m * n would not fit.
-int plan_q4_gemm_splits(const lgh_q4 *w, size_t m);
-hipError_t launch_q4_gemm(const lgh_q4 *w, const uint8_t *mxa, float *y, size_t m, int mode, float *part,
-                          size_t part_floats, hipStream_t stream);
+// GEMM on an activation operand image: y[j][m][n_j] (+)= x[m][k] . W[j]^T for
+// 1..3 matrices with the same k, one launch (the workgroups of all matrices
+// in one grid, one split-K reduce).  plan_q4_gemm_splits() is the number of K
+// splits the launch wants for m tokens; `part` holds part_floats floats of
+// scratch, and the launch uses fewer splits when splits * m * (sum of n)
+// would not fit.
+int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m);
+hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
+                          float *part, size_t part_floats, hipStream_t stream);
 
 // Test hooks.
 hipError_t launch_q4_block_dots(const uint8_t *qs, const int8_t *a, size_t nblocks, int32_t *out,

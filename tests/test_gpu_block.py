@@ -50,7 +50,9 @@ def _hidden(k, tokens, seed):
 
 @pytest.mark.parametrize("per_row", [False, True])
 @pytest.mark.parametrize("norm", [True, False])
-@pytest.mark.parametrize("tokens", [1, 3])
+# tokens: the one-launch GEMV, the M <= 4 batch kernel, the matrix-core batch kernel on one shared
+# activation image, the GEMM over all matrices in one launch (one split-K reduce).
+@pytest.mark.parametrize("tokens", [1, 3, 16, 100])
 @pytest.mark.parametrize("k,rows", BLOCKS)
 def test_norm_gemv_matches_oracle_and_op_sequence(gpu_ctx, oracle, k, rows, tokens, norm, per_row):
     gw, cw = _mats(gpu_ctx, oracle, k, rows, 500 + k + sum(rows))
