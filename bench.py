@@ -210,6 +210,33 @@ def q8_case(gb: GpuBench, iters, n=1536, k=1536):
             "frac_hbm": q8_bytes(n, k) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def q8_head_norm_case(gb: GpuBench, iters, n=65536, k=1536):
+    """The final rms_norm + Q8_0 head of a decode step (lfm2.rs:559-567): the norm fused into the
+    head's GEMV against rms_norm then q8_apply.  Rotating copies > 2x MALL."""
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    b8 = synth.q8_blocks(71, n, k)
+    count = math.ceil(2 * MALL_BYTES / (n * (k // 32) * 34))
+    mats = [q4.Q8Matrix.from_blocks(n, k, b8, gb.ctx) for _ in range(count)]
+    x = torch.from_numpy(synth.normal_f32(72, k)).cuda()
+    nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(73, k)).astype(np.float32)).cuda()
+    normed = torch.zeros(k, device="cuda")
+    y = torch.zeros(n, device="cuda")
+
+    def sequence(i):
+        q4.rms_norm(x, nw, 1e-5, normed, gb.ctx)
+        q4.q8_apply(mats[i % count], normed, 1, y)
+
+    ms_f = gb.timed(lambda i: q4.q8_norm_apply(mats[i % count], nw, 1e-5, x, 1, y), iters, 5)
+    ms_s = gb.timed(sequence, iters, 5)
+    for w in mats:
+        w.free()
+    byts = q8_bytes(n, k) + 4 * k
+    return {"n": n, "k": k, "us": ms_f * 1e3, "gbs": byts / (ms_f * 1e-3) / 1e9,
+            "frac_hbm": byts / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, "op_sequence_us": ms_s * 1e3}
+
+
 def q4_head_case(gb: GpuBench, iters, n=65536, k=1536):
     """Q4 GEMV over rotating copies (> 2x MALL); default: the tied-head shape (the alternative to
     the Q8_0 head)."""
@@ -467,6 +494,7 @@ def main():
         extra["q8_gemv_k1536_n1536"] = q8_case(gb, 200)
         log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
         extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
+        extra["final_norm_q8_head_k1536_n65536"] = q8_head_norm_case(gb, 20)
         extra["q4_head_k1536_n65536"] = q4_head_case(gb, 20)
         log("[bench] Q4 GEMV size sweep (launch floor -> HBM bound)")
         extra["q4_gemv_size_sweep"] = [

@@ -163,6 +163,16 @@ int lgh_q8_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *x, float *y, size_t 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev,
                     size_t tokens);
 
+/* The final rms_norm of a decode or prefill step followed by the Q8_0 output
+ * head (crates/llm-engine/src/lfm2.rs:559-567, 496-504): per token,
+ * y = W (rms_norm(hidden, norm_w, eps)), norm_w == NULL: y = W hidden -- the
+ * norm in the GEMV's prologue, one launch.  (A Q4 head takes lgh_q4_norm_gemv
+ * with one matrix.)  Results equal rms_norm followed by lgh_q8_gemv. */
+int lgh_q8_norm_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w, float eps, const float *hidden, float *y,
+                     size_t tokens);
+int lgh_q8_norm_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w_dev, float eps,
+                         const float *hidden_dev, float *y_dev, size_t tokens);
+
 /* ---- elementwise ops of the FFN block ----------------------------------------
  * rms_norm (crates/llm-cpu/src/ops.rs:8-23): out[r] = w * (x[r] * scale_r)
  * over `rows` rows of `dim`, scale_r = f32(1 / sqrt(sum_sq * (1/dim) + eps))

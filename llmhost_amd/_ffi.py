@@ -79,6 +79,8 @@ SIGNATURES = {
     "lgh_q4_ffn_gate_up": (_I, [_P, _P, _P, _P, C.c_float, _P, _P, _P, _P, _P, _P]),
     "lgh_q4_norm_gemv": (_I, [_P, _SZ, _P, _P, C.c_float, _P, _P, _SZ, _I]),
     "lgh_q4_norm_gemv_dev": (_I, [_P, _SZ, _P, _P, C.c_float, _P, _P, _SZ, _I]),
+    "lgh_q8_norm_gemv": (_I, [_P, _P, _P, C.c_float, _P, _P, _SZ]),
+    "lgh_q8_norm_gemv_dev": (_I, [_P, _P, _P, C.c_float, _P, _P, _SZ]),
 }
 
 _lib = None

@@ -568,7 +568,44 @@ int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_
   if (w->k > lgh::kQ8GemvMaxK) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", lgh::kQ8GemvMaxK);
   if (tokens > 65535) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports at most 65535 tokens per call");
   if (int r = set_device(ctx)) return r;
-  LGH_HIP(ctx, lgh::launch_q8_gemv(w, x_dev, y_dev, tokens, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_q8_gemv(w, x_dev, y_dev, tokens, nullptr, 0.0f, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q8_norm_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w_dev, float eps, const float *hidden_dev,
+                         float *y_dev, size_t tokens) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (tokens == 0 || w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && !hidden_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/y");
+  if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "hidden and norm weight must be 16-byte aligned");
+  if (w->k > lgh::kQ8GemvMaxK) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", lgh::kQ8GemvMaxK);
+  if (tokens > 65535) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports at most 65535 tokens per call");
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_q8_gemv(w, hidden_dev, y_dev, tokens, w->k ? norm_w_dev : nullptr, eps, ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q8_norm_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w, float eps, const float *hidden, float *y,
+                     size_t tokens) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (tokens == 0 || w->n == 0) return LGH_OK;
+  if (!y || (w->k && !hidden)) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/y");
+  if (int r = set_device(ctx)) return r;
+  Carve cv;
+  const size_t xb = tokens * w->k * sizeof(float), nb = w->k * sizeof(float), yb = tokens * w->n * sizeof(float);
+  const size_t ox = cv.take(xb), on = cv.take(norm_w ? nb : 0), oy = cv.take(yb);
+  if (int r = ensure(ctx, &ctx->stage, &ctx->stage_bytes, cv.off)) return r;
+  char *st = static_cast<char *>(ctx->stage);
+  float *xd = reinterpret_cast<float *>(st + ox), *nd = norm_w ? reinterpret_cast<float *>(st + on) : nullptr;
+  float *yd = reinterpret_cast<float *>(st + oy);
+  if (xb) LGH_HIP(ctx, hipMemcpyAsync(xd, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
+  if (norm_w && nb) LGH_HIP(ctx, hipMemcpyAsync(nd, norm_w, nb, hipMemcpyHostToDevice, ctx->stream));
+  if (int r = lgh_q8_norm_gemv_dev(ctx, w, nd, eps, xd, yd, tokens)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return LGH_OK;
 }
 

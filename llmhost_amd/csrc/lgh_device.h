@@ -349,6 +349,39 @@ __device__ __forceinline__ float rms_scale(double sumsq, double inv_dim, float e
   return static_cast<float>(1.0 / __builtin_sqrt(t));
 }
 
+// rms_norm of the x a GEMV-style workgroup holds in registers (thread t holds
+// float4s t + THREADS j; elements past k are 0 in x and in nw): the squares
+// summed in f64 (per thread, DPP tree per wave, then the wave sums in order),
+// scale = rms_scale(), then x = nw * (x * scale) in f32 (ops.rs:8-23).  All
+// threads must call it; it contains a workgroup barrier.
+template <int THREADS, int XJ>
+__device__ __forceinline__ void rms_norm_regs(float4 (&xv)[XJ], const float4 (&nv)[XJ], double inv_k, float eps,
+                                              double *s_ss) {
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const double x0 = xv[j].x, x1 = xv[j].y, x2 = xv[j].z, x3 = xv[j].w;
+    ss += x0 * x0;
+    ss += x1 * x1;
+    ss += x2 * x2;
+    ss += x3 * x3;
+  }
+  ss = wave_sum_dpp64(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0) s_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int i = 0; i < THREADS / kWave; i++) tot += s_ss[i];
+  const float scale = rms_scale(tot, inv_k, eps);
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    xv[j].x = nv[j].x * (xv[j].x * scale);
+    xv[j].y = nv[j].y * (xv[j].y * scale);
+    xv[j].z = nv[j].z * (xv[j].z * scale);
+    xv[j].w = nv[j].w * (xv[j].w * scale);
+  }
+}
+
 // ---- x -> LDS codes, shared by the GEMV-style kernels --------------------
 // Quantize the float4s held in registers (thread t holds x4[t + THREADS j])
 // into LDS: s_qs (natural order) and s_sa, for blocks [0, nblk).  All

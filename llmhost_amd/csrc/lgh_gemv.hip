@@ -169,32 +169,8 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
   }
 
-  // (2b) NORM: normed = nw * (x * scale); elements past k are 0 in x and nw.
-  if constexpr (NORM) {
-    double ss = 0.0;
-#pragma unroll
-    for (int j = 0; j < XJ; j++) {
-      const double x0 = xv[j].x, x1 = xv[j].y, x2 = xv[j].z, x3 = xv[j].w;
-      ss += x0 * x0;
-      ss += x1 * x1;
-      ss += x2 * x2;
-      ss += x3 * x3;
-    }
-    ss = wave_sum_dpp64(ss);
-    if (lane == 0) s_ss[wave] = ss;
-    __syncthreads();
-    double tot = 0.0;
-#pragma unroll
-    for (int i = 0; i < W; i++) tot += s_ss[i];
-    const float scale = rms_scale(tot, a.inv_k, a.eps);
-#pragma unroll
-    for (int j = 0; j < XJ; j++) {
-      xv[j].x = nv[j].x * (xv[j].x * scale);
-      xv[j].y = nv[j].y * (xv[j].y * scale);
-      xv[j].z = nv[j].z * (xv[j].z * scale);
-      xv[j].w = nv[j].w * (xv[j].w * scale);
-    }
-  }
+  // (2b) NORM: x = nw * (x * scale); elements past k are 0 in x and nw.
+  if constexpr (NORM) rms_norm_regs<THREADS, XJ>(xv, nv, a.inv_k, a.eps, s_ss);
 
   // (3) x -> LDS codes (chunks and scales past the row load as 0).
   if constexpr (PREQ) {
@@ -586,6 +562,9 @@ struct Q8GemvArgs {
   const uint16_t *sc;  // f16 scales [n][bpr]
   const float *x;      // [tokens][k]
   float *y;            // [tokens][n]
+  const float *nw;     // NORM: rms_norm weight [k]
+  double inv_k;        // NORM: 1 / k in f64 (ops.rs:12)
+  float eps;
   int n;
   int bpr;
 };
@@ -596,8 +575,10 @@ struct Q8GemvArgs {
 // one f16 scale per block, 8 v_dot4 against the LDS codes, and q8_apply's
 // per-block term (f32(dot) * sw) * sa added to the lane's sum
 // (weights.rs:206-212; the blocks are summed in a different order).  x is
-// always quantized per block (weights.rs:197); token blockIdx.y.
-template <int BPL, int KW, int W>
+// always quantized per block (weights.rs:197); token blockIdx.y.  NORM: each
+// token's row is rms_norm'd in the prologue first, as q4_gemv_kernel does (the
+// final norm before the output head, crates/llm-engine/src/lfm2.rs:559-567).
+template <int BPL, int KW, int W, bool NORM = false>
 __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;
@@ -609,6 +590,7 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   __shared__ __align__(16) int8_t s_qs[KB * 32];
   __shared__ float s_sa[KB];
   __shared__ float s_red[W];
+  __shared__ double s_ss[NORM ? W : 1];
   __shared__ float s_part[KW > 1 ? RG * 4 * KW : 1];
   const int bpr = a.bpr;
   const int tid = threadIdx.x;
@@ -623,20 +605,29 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
 
   // (1) x, then (1b) the x-before-weights barrier for long rows.
   const auto xr = make_rsrc(a.x + tok * static_cast<size_t>(bpr) * 32, static_cast<uint32_t>(bpr) * 128u);
+  const auto nr = make_rsrc(a.nw, NORM ? static_cast<uint32_t>(bpr) * 128u : 0u);
   float4 xv[XJ];
+  float4 nv[NORM ? XJ : 1];
   if constexpr (PAIRS) {
 #pragma unroll
     for (int j = 0; j < XP; j++) {
       const uint32_t off = static_cast<uint32_t>(tid + j * THREADS) * 32u;
       xv[2 * j] = buf_load_f4(xr, off);
       xv[2 * j + 1] = buf_load_f4(xr, off + 16u);
+      if constexpr (NORM) {
+        nv[2 * j] = buf_load_f4(nr, off);
+        nv[2 * j + 1] = buf_load_f4(nr, off + 16u);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   } else {
 #pragma unroll
-    for (int j = 0; j < XJ; j++) xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+    for (int j = 0; j < XJ; j++) {
+      xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+      if constexpr (NORM) nv[j] = buf_load_f4(nr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+    }
   }
 
   // (2) every weight load of this lane (rows past n fall outside the resource).
@@ -653,6 +644,9 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
     w1[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u : kOOB);
     s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
   }
+
+  // (2b) NORM: x = nw * (x * scale).
+  if constexpr (NORM) rms_norm_regs<THREADS, XJ>(xv, nv, a.inv_k, a.eps, s_ss);
 
   // (3) x -> LDS codes (per block).
   if constexpr (PAIRS)
@@ -922,16 +916,22 @@ hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float
 }
 
 // The Q8_0 GEMV takes the Q4 GEMV's plan (same row mapping, same limits).
-hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens, hipStream_t st) {
+hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
+                          hipStream_t st) {
   if (w->n == 0 || tokens == 0) return hipSuccess;
   const Q4GemvPlan p = plan_q4_gemv(w->n, w->bpr, 1, false);
   if (!p.ok || tokens > 65535) return hipErrorInvalidValue;  // rejected by the API before launch
-  Q8GemvArgs a{w->qs, w->sc, x, y, static_cast<int>(w->n), static_cast<int>(w->bpr)};
+  Q8GemvArgs a{w->qs, w->sc, x, y, norm_w, 1.0 / static_cast<double>(w->k), eps, static_cast<int>(w->n),
+               static_cast<int>(w->bpr)};
   const dim3 grid(static_cast<unsigned>(p.wgs_per_mat), static_cast<unsigned>(tokens));
-#define LGH_Q8(BB, KK, WW)                                                                  \
-  if (p.BPL == BB && p.KW == KK && p.W == WW) {                                             \
-    hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW>), grid, dim3(WW * kWave), 0, st, a);      \
-    return hipGetLastError();                                                               \
+  const bool norm = norm_w != nullptr;
+#define LGH_Q8(BB, KK, WW)                                                                            \
+  if (p.BPL == BB && p.KW == KK && p.W == WW) {                                                       \
+    if (norm)                                                                                         \
+      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, true>), grid, dim3(WW * kWave), 0, st, a);       \
+    else                                                                                              \
+      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, false>), grid, dim3(WW * kWave), 0, st, a);      \
+    return hipGetLastError();                                                                         \
   }
   LGH_Q8(1, 1, 16);
   LGH_Q8(1, 1, 8);

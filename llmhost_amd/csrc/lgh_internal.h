@@ -175,9 +175,10 @@ hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row,
                                 float *row_scale, hipStream_t stream);
 hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
                               int mode, hipStream_t stream);
-// Q8_0 GEMV for k <= kQ8GemvMaxK (the Q4 GEMV plan's reach).
+// Q8_0 GEMV for k <= kQ8GemvMaxK (the Q4 GEMV plan's reach); with norm_w not
+// null each token's row is rms_norm'd in the prologue (eps as rms_norm).
 constexpr size_t kQ8GemvMaxK = 32768;
-hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens,
+hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
                           hipStream_t stream);
 
 // Batched activation quantization: x[m][k] -> qs[m][k], scales[m][k/32]

@@ -514,6 +514,23 @@ def q8_apply(m: Q8Matrix, x, tokens: int, out) -> None:
     ctx.check(lib().lgh_q8_gemv(ctx.handle, m.handle, _np_ptr(x), _np_ptr(out), tokens))
 
 
+def q8_norm_apply(m: Q8Matrix, norm_w, eps: float, hidden, tokens: int, out) -> None:
+    """The final rms_norm then the Q8_0 head (crates/llm-engine/src/lfm2.rs:559-567): per token
+    out = W rms_norm(hidden, norm_w, eps) (norm_w None: no norm), the norm in the GEMV's prologue."""
+    ctx = m.ctx
+    if _is_torch(hidden):
+        _shape_assert(hidden.numel() == tokens * m.k and out.numel() == tokens * m.n, "length mismatch")
+        nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
+        ctx.check(lib().lgh_q8_norm_gemv_dev(ctx.handle, m.handle, nw, float(eps), _dev_ptr(hidden, "hidden"),
+                                             _dev_ptr(out, "out"), tokens))
+        return
+    hidden = _host_f32(hidden, "hidden")
+    out = _host_f32(out, "out")
+    _shape_assert(hidden.size == tokens * m.k and out.size == tokens * m.n, "length mismatch")
+    nw = None if norm_w is None else _np_ptr(_host_f32(norm_w, "norm_w"))
+    ctx.check(lib().lgh_q8_norm_gemv(ctx.handle, m.handle, nw, float(eps), _np_ptr(hidden), _np_ptr(out), tokens))
+
+
 # ---- test hooks ---------------------------------------------------------------------
 def q4_block_dots(blocks: np.ndarray, a: np.ndarray, ctx: Context | None = None) -> np.ndarray:
     """Device per-block dots nibble(W) . a (dot_q4_q8_scalar, gemv_q4.rs:959-966)."""

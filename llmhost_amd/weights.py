@@ -125,3 +125,11 @@ class OutputHead:
             self.linear.apply(x, tokens, out)
         else:
             _q4.q8_apply(self.q8, x, tokens, out)
+
+    def norm_apply(self, norm_w, eps: float, hidden, tokens: int, out) -> None:
+        """`normed = rms_norm(hidden)` then `self.apply(normed)` (lfm2.rs:559-567, 496-504), the
+        norm fused into the head's GEMV."""
+        if self.linear is not None:
+            _q4.norm_gemv([self.linear.mat], norm_w, eps, hidden, [out], tokens)
+        else:
+            _q4.q8_norm_apply(self.q8, norm_w, eps, hidden, tokens, out)

@@ -173,3 +173,29 @@ def test_seam_mirror_block_sides(gpu_ctx, oracle):
     assert np.array_equal(h2.view(np.uint32), (hidden + proj).view(np.uint32))
     with pytest.raises(LghShapeError):
         weights.apply_then_add_inplace(wo, outs[1], 1, h2)
+
+
+@pytest.mark.parametrize("tokens", [1, 2])
+@pytest.mark.parametrize("n,k", [(4096, 1536), (96, 64), (130, 2048), (64, 8192)])
+def test_q8_head_with_final_norm(gpu_ctx, oracle, n, k, tokens):
+    """rms_norm + the Q8_0 head in one launch: bit-identical to lgh_rms_norm then lgh_q8_gemv, and
+    within tolerance of the oracle's rms_norm then q8_apply (lfm2.rs:559-567)."""
+    from llmhost_amd import weights
+
+    b8 = synth.q8_blocks(960 + n, n, k)
+    w8 = q4.Q8Matrix.from_blocks(n, k, b8, gpu_ctx)
+    hidden, nw = _hidden(k, tokens, 961 + k)
+    got = np.full(tokens * n, np.nan, dtype=np.float32)
+    weights.OutputHead(q8=w8).norm_apply(nw, EPS, hidden, tokens, got)
+    normed = np.zeros_like(hidden)
+    q4.rms_norm(hidden, nw, EPS, normed, gpu_ctx)
+    seq = np.zeros(tokens * n, dtype=np.float32)
+    q4.q8_apply(w8, normed, tokens, seq)
+    assert np.array_equal(got.view(np.uint32), seq.view(np.uint32))
+    ref = oracle.q8_apply(b8, n, k, oracle.rms_norm(hidden, nw, EPS), tokens, threads=8)
+    assert_close(got, ref.ravel(), what="q8 head")
+    plain = np.zeros(tokens * n, dtype=np.float32)
+    q4.q8_norm_apply(w8, None, EPS, hidden, tokens, plain)
+    direct = np.zeros(tokens * n, dtype=np.float32)
+    q4.q8_apply(w8, hidden, tokens, direct)
+    assert np.array_equal(plain.view(np.uint32), direct.view(np.uint32))
