@@ -343,6 +343,54 @@ def block_input_case(gb: GpuBench, iters, rows, dim=1536, tokens=1):
             "tops": ops / (ms_f * 1e-3) / 1e12, "op_sequence_us": ms_s * 1e3, "bytes": byts}
 
 
+def decode_step_case(gb: GpuBench, iters, layers=16, dim=1536, inter=8192, vocab=65536):
+    """The matmul side of a 16-layer decode step, chained as the engine runs it (lfm2.rs:559-567,
+    784-911): per layer rms_norm + q / k / v (1536, 256, 256 rows: the sweep's qkv 1536x2048) in
+    one launch, the output projection added onto hidden in f32 (its input stands in for the
+    attention output: the layer's q), the fused FFN block; then the final rms_norm + Q8_0 head.
+    Every call reads what the previous one wrote.  One weight set (391 MB of Q4 layers + 107 MB
+    of head > 2x MALL, so each step streams from HBM)."""
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    raw = {}
+
+    def mat(n, k, j):
+        key = (n, k, j)
+        if key not in raw:
+            raw[key] = torch.from_numpy(synth.q4_blocks(800 + j, n, k).view(np.uint8).copy()).cuda()
+        return q4.Q4Matrix.from_blocks(n, k, raw[key], gb.ctx)
+
+    L = [{"q": mat(dim, dim, 0), "k": mat(256, dim, 1), "v": mat(256, dim, 2), "o": mat(dim, dim, 3),
+          "w1": mat(inter, dim, 4), "w3": mat(inter, dim, 5), "w2": mat(dim, inter, 6)} for _ in range(layers)]
+    raw.clear()
+    head = q4.Q8Matrix.from_blocks(vocab, dim, synth.q8_blocks(810, vocab, dim), gb.ctx)
+    nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(811, dim)).astype(np.float32)).cuda()
+    hidden0 = torch.from_numpy(synth.normal_f32(812, dim)).cuda()
+    hidden = hidden0.clone()
+    q, k, v = torch.zeros(dim, device="cuda"), torch.zeros(256, device="cuda"), torch.zeros(256, device="cuda")
+    logits = torch.zeros(vocab, device="cuda")
+
+    def step(_):
+        hidden.copy_(hidden0)
+        for m in L:
+            q4.norm_gemv([m["q"], m["k"], m["v"]], nw, 1e-5, hidden, [q, k, v])
+            q4.apply_add_inplace(m["o"], q, hidden)
+            q4.ffn_residual(m["w1"], m["w3"], m["w2"], nw, 1e-5, hidden)
+        q4.q8_norm_apply(head, nw, 1e-5, hidden, 1, logits)
+
+    ms = gb.timed(step, iters, 2)
+    layer_bytes = sum(w.n * (w.k // 32) * 18 for w in L[0].values())
+    total = layers * layer_bytes + vocab * (dim // 32) * 34
+    for m in L:
+        for w in m.values():
+            w.free()
+    head.free()
+    return {"layers": layers, "us": ms * 1e3, "weight_bytes": total, "gbs": total / (ms * 1e-3) / 1e9,
+            "frac_hbm": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "launches": 4 * layers + 2,
+            "tokens_per_s": 1e3 / ms}
+
+
 def cpu_baseline(target_s: float = 12.0):
     """The oracle's llm-cpu restatement (runtime-dispatched kernel, pinned
     pool) on this host, over rotating packed copies larger than the LLC."""
@@ -495,6 +543,8 @@ def main():
         log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
         extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
         extra["final_norm_q8_head_k1536_n65536"] = q8_head_norm_case(gb, 20)
+        log("[bench] chained 16-layer decode step (fused entry points)")
+        extra["decode_step_16L_chained"] = decode_step_case(gb, 10)
         extra["q4_head_k1536_n65536"] = q4_head_case(gb, 20)
         log("[bench] Q4 GEMV size sweep (launch floor -> HBM bound)")
         extra["q4_gemv_size_sweep"] = [
