@@ -15,6 +15,8 @@
 //   * 4 DPP adds give every lane of a DPP row its row's slice sum; slice sums
 //     meet in LDS and are added in slice order (deterministic), then Assign
 //     or AddF64 (gemv_q4.rs:486-497) after removing the x16 (exact).
+#include <type_traits>
+
 #include "lgh_device.h"
 #include "lgh_internal.h"
 
@@ -396,8 +398,13 @@ struct MmaChunk {
   static constexpr int SL = CB / 4;  // scale loads per lane
   uint4 wv[WL];
   uint16_t sv[SL];
+  // One token tile forms the scale products on the matrix core (an f32
+  // outer-product MFMA per block quad); two or four do them on the VALU.
+  static constexpr bool kOuter = TT == 1;
   uint4 bq[TT][CB / 2];  // B operands of block pairs
-  float4 sa[TT][CB / 4];  // activation scales of block quads (token lane % 16)
+  // Activation scales per block quad: of token lane % 16 and block
+  // 4 quad + lane / 16 (kOuter), else of token lane % 16 and all 4 blocks.
+  std::conditional_t<kOuter, float, float4> sa[TT][CB / 4];
 };
 
 // Issue every load of chunk ch: weights (piece p = 64 i + lane is row p / CB,
@@ -433,15 +440,26 @@ __device__ __forceinline__ void mma_load(const Q4MmaArgs &a, __amdgpu_buffer_rsr
 #pragma unroll
     for (int j = 0; j < CB / 4; j++) {
       const int qd = kb0 / 4 + j;  // block quad
-      c.sa[tt][j] = buf_load_f4(ar, tile && qd < a.pq ? static_cast<uint32_t>((tt * a.pq + qd) * 16 + lr) * 16u : kOOB);
+      const uint32_t rec = static_cast<uint32_t>((tt * a.pq + qd) * 16 + lr) * 16u;  // token lr's 4 scales
+      const bool in = tile && qd < a.pq;
+      if constexpr (C::kOuter)
+        c.sa[tt][j] = buf_load_f32(ar, in ? rec + 4u * static_cast<uint32_t>(lane >> 4) : kOOB);
+      else
+        c.sa[tt][j] = buf_load_f4(ar, in ? rec : kOOB);
     }
   }
 }
 
 // Transpose the chunk's weights and scales through this wave's LDS tile
 // (the same wave writes and reads it: LDS keeps a wave's accesses in order),
-// then one MFMA and 4 folds per block and token tile.  Blocks past the row
-// hold zero weights, scales and codes and add exactly 0 (no branches).
+// then per block one int8 MFMA and 4 folds per token tile.  The scale
+// products sw[row] * sa[token]: with one token tile, one f32 MFMA per block
+// quad (v_mfma_f32_16x16x1_4b_f32: block j in elements 4j..4j+3, laid out
+// like the block dots -- lane l = token l%16, rows 4(l/16)..+3), which
+// replaces 16 VALU multiplies (M=16, K=2048, N=8192: 8.05 -> 7.69 us); with
+// two or four token tiles the extra matrix-core passes cost as much as they
+// save (measured), so the VALU multiplies stay.  Blocks past the row hold
+// zero weights, scales and codes and add exactly 0 (no branches).
 template <int TT, int CB>
 __device__ __forceinline__ void mma_compute(const MmaChunk<TT, CB> &c, uint32_t *tw, float *tsw,
                                             float (&acc)[TT][4]) {
@@ -455,25 +473,48 @@ __device__ __forceinline__ void mma_compute(const MmaChunk<TT, CB> &c, uint32_t 
   }
 #pragma unroll
   for (int e = 0; e < C::SL; e++) tsw[(C::SL * (lane & 3) + e) * 16 + (lane >> 2)] = h2f(c.sv[e]);
+  const v4i32 zero = {0, 0, 0, 0};
 #pragma unroll
-  for (int b = 0; b < CB; b++) {
-    const uint32_t dw = tw[lr * RS + b * 4 + g];
-    const long wa = static_cast<long>(static_cast<uint32_t>(nib_lo16(dw))) |
-                    (static_cast<long>(static_cast<uint32_t>(nib_hi16(dw))) << 32);
-    const float4 sw = *reinterpret_cast<const float4 *>(&tsw[b * 16 + 4 * g]);
+  for (int q = 0; q < CB / 4; q++) {
+    long wa[4];
 #pragma unroll
-    for (int tt = 0; tt < TT; tt++) {
-      const uint4 bp = c.bq[tt][b / 2];
-      const long wb = (b & 1) ? (static_cast<long>(bp.z) | (static_cast<long>(bp.w) << 32))
-                              : (static_cast<long>(bp.x) | (static_cast<long>(bp.y) << 32));
-      const v4i32 zero = {0, 0, 0, 0};
-      const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, wb, zero, 0, 0, 0);
-      const float4 s4 = c.sa[tt][b / 4];
-      const float s = (b & 3) == 0 ? s4.x : (b & 3) == 1 ? s4.y : (b & 3) == 2 ? s4.z : s4.w;
-      acc[tt][0] = fmaf(static_cast<float>(d[0]), sw.x * s, acc[tt][0]);
-      acc[tt][1] = fmaf(static_cast<float>(d[1]), sw.y * s, acc[tt][1]);
-      acc[tt][2] = fmaf(static_cast<float>(d[2]), sw.z * s, acc[tt][2]);
-      acc[tt][3] = fmaf(static_cast<float>(d[3]), sw.w * s, acc[tt][3]);
+    for (int j = 0; j < 4; j++) {
+      const uint32_t dw = tw[lr * RS + (4 * q + j) * 4 + g];
+      wa[j] = static_cast<long>(static_cast<uint32_t>(nib_lo16(dw))) |
+              (static_cast<long>(static_cast<uint32_t>(nib_hi16(dw))) << 32);
+    }
+    if constexpr (C::kOuter) {
+      const v16f zero16 = {};
+      const float swq = tsw[(4 * q + g) * 16 + lr];  // row lr, block 4q + g
+      const v16f P = __builtin_amdgcn_mfma_f32_16x16x1f32(swq, c.sa[0][q], zero16, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint4 bp = c.bq[0][2 * q + j / 2];
+        const long wb = (j & 1) ? (static_cast<long>(bp.z) | (static_cast<long>(bp.w) << 32))
+                                : (static_cast<long>(bp.x) | (static_cast<long>(bp.y) << 32));
+        const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa[j], wb, zero, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[0][v] = fmaf(static_cast<float>(d[v]), P[4 * j + v], acc[0][v]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int b = 4 * q + j;
+        const float4 sw = *reinterpret_cast<const float4 *>(&tsw[b * 16 + 4 * g]);
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+          const uint4 bp = c.bq[tt][b / 2];
+          const long wb = (b & 1) ? (static_cast<long>(bp.z) | (static_cast<long>(bp.w) << 32))
+                                  : (static_cast<long>(bp.x) | (static_cast<long>(bp.y) << 32));
+          const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa[j], wb, zero, 0, 0, 0);
+          const float4 s4 = c.sa[tt][q];
+          const float s = j == 0 ? s4.x : j == 1 ? s4.y : j == 2 ? s4.z : s4.w;
+          acc[tt][0] = fmaf(static_cast<float>(d[0]), sw.x * s, acc[tt][0]);
+          acc[tt][1] = fmaf(static_cast<float>(d[1]), sw.y * s, acc[tt][1]);
+          acc[tt][2] = fmaf(static_cast<float>(d[2]), sw.z * s, acc[tt][2]);
+          acc[tt][3] = fmaf(static_cast<float>(d[3]), sw.w * s, acc[tt][3]);
+        }
+      }
     }
   }
 }
