@@ -22,7 +22,8 @@
 // K advances one block pair per stage.  A stage is the verbatim concatenation
 // of NS weight records and MS activation records (lgh_internal.h), copied
 // global -> LDS by buffer_load ... lds (DMA: no registers, no VALU) into one
-// of three LDS buffers; stages p+1 and p+2 are in flight while stage p is
+// of three LDS buffers (two for launches of many rounds, which then hold 5
+// waves per SIMD); stages p+1 and p+2 (p+1) are in flight while stage p is
 // computed, one barrier per stage.
 #include "lgh_device.h"
 #include "lgh_internal.h"
@@ -36,6 +37,7 @@ constexpr int kWRec = static_cast<int>(kMxWRec);
 constexpr int kARec = static_cast<int>(kMxARec);
 constexpr int kTile = static_cast<int>(kMxTile);
 constexpr long kSplitTarget = 512;  // two workgroups per CU (M=512, K=10752, N=2048: 61.5 -> 48.6 us vs one)
+constexpr long kFiveWaveWgs = 5120;  // four rounds of 5 workgroups on each of 256 CUs
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]
@@ -155,16 +157,55 @@ __device__ __forceinline__ void dma_stage(const GemmArgs &g, const Slots<C> &s, 
   }
 }
 
+// Per-thread LDS byte offsets (from a stage buffer's start) of a wave's
+// operand reads, built once and kept opaque: every read is then one base
+// VGPR plus a constant (buffer, tile, block), so the whole pipeline holds 10
+// address VGPRs instead of one per buffer and read.  Blocks 0 and 1 have
+// bases of their own, so the compiler does not pair their reads into one
+// ds_read2 whose result would then be split into the two operands by v_mov.
+struct StageOffs {
+  int a16[2], a8[2];  // weight operand rows (plane0, plane1) of blocks 0 and 1, tile tn = 0
+  int b16[2], b8[2];  // activation operand rows (h or l half) of blocks 0 and 1, tile tm = 0
+  int ws, as;         // weight / activation scale arrays
+};
+
+template <class C, int TN, int TM>
+__device__ __forceinline__ StageOffs stage_offsets(int wn, int wm) {
+  const int lane = threadIdx.x & 63, row = lane & 31, half = lane >> 5;
+  const int wrec = wn * TN * kWRec, arec = C::A_LDS + wm * TM * kARec;
+  StageOffs o;
+#pragma unroll
+  for (int b = 0; b < 2; b++) {
+    o.a16[b] = opaque(wrec + b * kTile + row * 16);
+    o.a8[b] = opaque(wrec + b * kTile + 512 + row * 8);
+    o.b16[b] = opaque(arec + (2 * b + half) * kTile + row * 16);
+    o.b8[b] = opaque(arec + (2 * b + half) * kTile + 512 + row * 8);
+  }
+  o.ws = opaque(wrec + 2 * kTile + lane * 4);
+  o.as = opaque(arec + 4 * kTile + lane * 4);
+  return o;
+}
+
+__device__ __forceinline__ v8i mx_operand(const char *p16, const char *p8) {
+  const uint4 p0 = *reinterpret_cast<const uint4 *>(p16);
+  const uint2 p1 = *reinterpret_cast<const uint2 *>(p8);
+  v8i r;
+  r[0] = static_cast<int>(p0.x);
+  r[1] = static_cast<int>(p0.y);
+  r[2] = static_cast<int>(p0.z);
+  r[3] = static_cast<int>(p0.w);
+  r[4] = static_cast<int>(p1.x);
+  r[5] = static_cast<int>(p1.y);
+  r[6] = 0;
+  r[7] = 0;
+  return r;
+}
+
 // One stage of the inner loop for a wave's TN x TM tiles: per tile, the
 // outer product of the two blocks' scales, the two blocks' exact dots, and
 // 32 FMAs folding them into the accumulators (block order as in the reference).
-// r16 / r8 = row * 16 / row * 8 for the second block's reads, opaque so the
-// compiler does not pair them with the first block's into one ds_read2 whose
-// result would then be split into the two operands by v_mov.
 template <class C, int TN, int TM>
-__device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, int r16, int r8,
-                                              float (&acc)[TN][TM][16]) {
-  const int lane = threadIdx.x & 63, row = lane & 31, half = lane >> 5;
+__device__ __forceinline__ void compute_stage(const char *buf, const StageOffs &o, float (&acc)[TN][TM][16]) {
   const v32f zero32 = {};
   // The scale outer products go first: lane L holds block L/32, row or token
   // L%32 of the record's f32 scale array [block][row] (read linearly).  Their
@@ -173,26 +214,20 @@ __device__ __forceinline__ void compute_stage(const char *buf, int wn, int wm, i
   float xs[TN], ys[TM];
   v8i A[2][TN], B[2][TM];
 #pragma unroll
-  for (int tn = 0; tn < TN; tn++) xs[tn] = reinterpret_cast<const float *>(buf + (wn * TN + tn) * kWRec + 2 * kTile)[lane];
+  for (int tn = 0; tn < TN; tn++) xs[tn] = *reinterpret_cast<const float *>(buf + o.ws + tn * kWRec);
 #pragma unroll
-  for (int tm = 0; tm < TM; tm++)
-    ys[tm] = reinterpret_cast<const float *>(buf + C::A_LDS + (wm * TM + tm) * kARec + 4 * kTile)[lane];
+  for (int tm = 0; tm < TM; tm++) ys[tm] = *reinterpret_cast<const float *>(buf + o.as + tm * kARec);
   v32f P[TN][TM];
 #pragma unroll
   for (int tn = 0; tn < TN; tn++)
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) P[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x1f32(xs[tn], ys[tm], zero32, 0, 0, 0);
 #pragma unroll
-  for (int tn = 0; tn < TN; tn++) {
-    const char *rec = buf + (wn * TN + tn) * kWRec;
-    A[0][tn] = mx_row(rec, row);
-    A[1][tn] = mx_row_at(rec + kTile, r16, r8);
-  }
+  for (int b = 0; b < 2; b++) {
 #pragma unroll
-  for (int tm = 0; tm < TM; tm++) {
-    const char *rec = buf + C::A_LDS + (wm * TM + tm) * kARec;
-    B[0][tm] = mx_row(rec + half * kTile, row);
-    B[1][tm] = mx_row_at(rec + (2 + half) * kTile, r16, r8);
+    for (int tn = 0; tn < TN; tn++) A[b][tn] = mx_operand(buf + o.a16[b] + tn * kWRec, buf + o.a8[b] + tn * kWRec);
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) B[b][tm] = mx_operand(buf + o.b16[b] + tm * kARec, buf + o.b8[b] + tm * kARec);
   }
 #pragma unroll
   for (int tn = 0; tn < TN; tn++)
@@ -226,34 +261,32 @@ __device__ __forceinline__ void wait_vm_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
-// Stage p, held in `cur`; `nxt2` (read during stage p-1) receives stage p+2.
-// The wait leaves only stage p+1's DMAs of this wave in flight; after the
-// barrier every wave's DMAs of stage p are complete and every wave is done
-// reading `nxt2`.
-template <class C, int TN, int TM>
+// Stage p, held in `cur`; `nxt` (read during stage p-1) receives stage
+// p+NB-1.  The wait leaves only stages p+1..p+NB-2's DMAs of this wave in
+// flight; after the barrier every wave's DMAs of stage p are complete and
+// every wave is done reading `nxt`.
+template <class C, int TN, int TM, int NB>
 __device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int wave, int p, int pend,
-                                              const char *cur, char *nxt2, int wn, int wm, int r16, int r8,
+                                              const char *cur, char *nxt, const StageOffs &o,
                                               float (&acc)[TN][TM][16]) {
-  wait_vm_barrier<C::WPW>();
-  dma_stage<C>(g, slots, wave, p + 2, pend, nxt2);
-  compute_stage<C, TN, TM>(cur, wn, wm, r16, r8, acc);
+  wait_vm_barrier<(NB - 2) * C::WPW>();
+  dma_stage<C>(g, slots, wave, p + NB - 1, pend, nxt);
+  compute_stage<C, TN, TM>(cur, o, acc);
   // Keep each stage's MFMAs and folds inside the stage: interleaving them
   // with the next stage's only lengthens register lifetimes.
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int WN, int WM, int TN, int TM>
-__global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmMulti gm) {
+// NB stage buffers (prefetch distance NB - 1); WPE waves per SIMD.
+template <int WN, int WM, int TN, int TM, int NB, int WPE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemm_mx_kernel(
+    GemmMulti gm) {
   using C = Cfg<WN, WM, TN, TM>;
-  // Three stage buffers as distinct objects, so the compiler can tell the
-  // buffer being read from the ones the DMA is filling.
-  __shared__ __align__(1024) char lds0[C::STAGE];
-  __shared__ __align__(1024) char lds1[C::STAGE];
-  __shared__ __align__(1024) char lds2[C::STAGE];
-  const int lane = threadIdx.x & 63;
+  // NB stage buffers in one array, indexed by compile-time constants only:
+  // a buffer's reads are the per-thread offsets plus a constant.
+  __shared__ __align__(1024) char lds[NB][C::STAGE];
   const int wave = uniform(threadIdx.x >> 6);
   const int wn = wave % WN, wm = wave / WN;
-  const int row = lane & 31, half = lane >> 5;
   int bx = blockIdx.x, mat = 0;
   if (bx >= gm.gx0) {
     bx -= gm.gx0;
@@ -265,6 +298,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmMulti gm) {
   }
   const GemmArgs &g = gm.g[uniform(mat)];
   const int nt0 = bx * C::NS, mt0 = blockIdx.y * C::MS;
+  const int lane = threadIdx.x & 63, row = lane & 31, half = lane >> 5;
 
   float acc[TN][TM][16];
 #pragma unroll
@@ -276,22 +310,24 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_mx_kernel(GemmMulti gm) {
 
   Slots<C> slots;
   init_slots<C>(g, wave, nt0, mt0, slots);
-  const int r16 = opaque(row * 16), r8 = opaque(row * 8);
+  const StageOffs offs = stage_offsets<C, TN, TM>(wn, wm);
   // Split z of the K range: block pairs [p0, pend).
   const int z = blockIdx.z;
   const int p0 = static_cast<int>(static_cast<long>(g.pp) * z / g.splits);
   const int pend = static_cast<int>(static_cast<long>(g.pp) * (z + 1) / g.splits);
-  dma_stage<C>(g, slots, wave, p0, pend, lds0);
-  dma_stage<C>(g, slots, wave, p0 + 1, pend, lds1);
-  // Unrolled by three so every stage's buffer roles are static.
+#pragma unroll
+  for (int u = 0; u < NB - 1; u++) dma_stage<C>(g, slots, wave, p0 + u, pend, lds[u]);
+  // Unrolled by NB so every stage's buffer roles are static.
   int p = p0;
-  for (; p + 2 < pend; p += 3) {
-    pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, r16, r8, acc);
-    pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, r16, r8, acc);
-    pipeline_step<C, TN, TM>(g, slots, wave, p + 2, pend, lds2, lds1, wn, wm, r16, r8, acc);
+  for (; p + NB - 1 < pend; p += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; u++)
+      pipeline_step<C, TN, TM, NB>(g, slots, wave, p + u, pend, lds[u], lds[(u + NB - 1) % NB], offs, acc);
   }
-  if (p < pend) pipeline_step<C, TN, TM>(g, slots, wave, p, pend, lds0, lds2, wn, wm, r16, r8, acc);
-  if (p + 1 < pend) pipeline_step<C, TN, TM>(g, slots, wave, p + 1, pend, lds1, lds0, wn, wm, r16, r8, acc);
+#pragma unroll
+  for (int u = 0; u < NB - 1; u++)
+    if (p + u < pend)
+      pipeline_step<C, TN, TM, NB>(g, slots, wave, p + u, pend, lds[u], lds[(u + NB - 1) % NB], offs, acc);
   // Drain the prefetches of stages past pend before the workgroup can exit
   // (their LDS must not be written after it is released).
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
@@ -396,18 +432,7 @@ int splits_for_tiles(long tiles, size_t pp) {
   return splits;
 }
 
-template <int WN, int WM, int TN, int TM>
-int splits_for(size_t nt, size_t mt, size_t pp) {
-  using C = Cfg<WN, WM, TN, TM>;
-  const long tiles = static_cast<long>((nt + C::NS - 1) / C::NS) * static_cast<long>((mt + C::MS - 1) / C::MS);
-  // Split K when the tiles alone leave CUs idle: aim for >= kSplitTarget
-  // workgroups while keeping >= 8 block pairs per split.
-  int splits = 1;
-  while (tiles * splits < kSplitTarget && pp / (2 * splits) >= 8) splits *= 2;
-  return splits;
-}
-
-template <int WN, int WM, int TN, int TM>
+template <int WN, int WM, int TN, int TM, int NB, int WPE>
 hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
   using C = Cfg<WN, WM, TN, TM>;
   int gx[3] = {0, 0, 0};
@@ -418,7 +443,7 @@ hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
   gm.gx0 = gx[0];
   gm.gx1 = gx[1];
   const dim3 grid(static_cast<unsigned>(gx[0] + gx[1] + gx[2]), (gm.g[0].mt + C::MS - 1) / C::MS, splits);
-  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM>), grid, dim3(kThreads), 0, st, gm);
+  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM, NB, WPE>), grid, dim3(kThreads), 0, st, gm);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   ReduceMulti r{};
@@ -445,12 +470,15 @@ hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
 // fast as or faster than 128 x 64 and 128 x 128 -- the inner loop is bound by
 // the matrix core plus the fold (which do not overlap on gfx950), and the
 // small tile keeps the most workgroups resident to cover the stage loads.
-int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m) {
+static long gemm_tiles(const lgh_q4 *const *w, int nmat, size_t m) {
   using C = Cfg<4, 1, 1, 1>;
   long tiles = 0;
   for (int j = 0; j < nmat; j++) tiles += static_cast<long>((w[j]->nt + C::NS - 1) / C::NS);
-  tiles *= static_cast<long>(((m + 31) / 32 + C::MS - 1) / C::MS);
-  return splits_for_tiles<4, 1, 1, 1>(tiles, w[0]->pp);
+  return tiles * static_cast<long>(((m + 31) / 32 + C::MS - 1) / C::MS);
+}
+
+int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m) {
+  return splits_for_tiles<4, 1, 1, 1>(gemm_tiles(w, nmat, m), w[0]->pp);
 }
 
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
@@ -481,7 +509,14 @@ hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, 
                        static_cast<uint32_t>(mt * w[j]->pp * kMxARec)};
     off += w[j]->n;
   }
-  return launch_cfg<4, 1, 1, 1>(gm, nmat, splits, st);
+  // Launches of many rounds run the two-buffer pipeline (24 KB of LDS) at 5
+  // waves per SIMD (96 VGPRs): M=2048, K=2048, N=10752 (5376 workgroups)
+  // 144.6-149.6 -> 134.3-137.4 us.  Shorter launches keep three buffers at 4
+  // waves per SIMD: M=512, K=2048, N=10752 (1344 workgroups) takes 43.4 us
+  // with the 5-wave form against 41.1 us, M=2048, K=10752, N=2048 (1024) 146
+  // against 141.6 us.
+  if (splits == 1 && gemm_tiles(w, nmat, m) >= kFiveWaveWgs) return launch_cfg<4, 1, 1, 1, 2, 5>(gm, nmat, 1, st);
+  return launch_cfg<4, 1, 1, 1, 3, 4>(gm, nmat, splits, st);
 }
 
 hipError_t launch_q4_mfma_block_dots(const lgh_q4 *w, const uint8_t *mxa, size_t m, int32_t *out,

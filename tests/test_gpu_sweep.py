@@ -54,3 +54,28 @@ def test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, seed):
     else:
         ref = y0 + prod
     assert_close(got, ref, what=f"m={m} n={n} k={k} mode={mode} per_row={per_row}")
+
+
+# Launches of >= 5120 workgroups (128-row x 32-token tiles, summed over the matrices of one call)
+# without split K take the two-buffer, 5-waves-per-SIMD form of the GEMM kernel.  Short K keeps
+# the oracle fast; ragged M, N and an odd block count cover the tile and pair tails.
+FIVE_WAVE = [(2048, 10752, 64), (2000, 10700, 96)]
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("m,n,k", FIVE_WAVE)
+def test_gemm_five_wave_route(gpu_ctx, oracle, m, n, k, mode, per_row):
+    test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 31 * m + n + k + mode)
+
+
+def test_gemm_five_wave_route_three_matrices(gpu_ctx, oracle):
+    k, rows, tokens = 64, (4096, 4096, 2560), 2048  # 84 N groups x 64 token tiles
+    bl = [synth.q4_blocks(60 + j, n, k) for j, n in enumerate(rows)]
+    gw = [q4.Q4Matrix.from_blocks(n, k, b, gpu_ctx) for n, b in zip(rows, bl)]
+    x = synth.activations(64, tokens, k)
+    outs = [np.full(tokens * n, np.nan, dtype=np.float32) for n in rows]
+    q4.norm_gemv(gw, None, 1e-5, x, outs, tokens)
+    for j, (o, n, b) in enumerate(zip(outs, rows, bl)):
+        ref = oracle.gemm_q4(oracle.Q4Matrix(n, k, b), x, tokens, kernel=oracle.KERNEL_SCALAR, threads=8)
+        assert_close(o, ref.ravel(), what=f"matrix {j}")
