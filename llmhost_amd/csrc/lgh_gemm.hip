@@ -37,6 +37,8 @@ constexpr int kWRec = static_cast<int>(kMxWRec);
 constexpr int kARec = static_cast<int>(kMxARec);
 constexpr int kTile = static_cast<int>(kMxTile);
 constexpr long kSplitTarget = 512;  // two workgroups per CU (M=512, K=10752, N=2048: 61.5 -> 48.6 us vs one)
+constexpr size_t kSplitMinPairs = 64;  // K >= 4096
+constexpr size_t kSplitPairs = 16;     // K >= 1024 per split
 constexpr long kFiveWaveWgs = 5120;  // four rounds of 5 workgroups on each of 256 CUs
 
 struct GemmArgs {
@@ -423,12 +425,19 @@ __global__ __launch_bounds__(256) void splitk_reduce_multi_kernel(ReduceMulti r)
   y[e] = r.mode == LGH_ASSIGN ? v : apply_mode(y[e], v, r.mode);
 }
 
+// Split K when the tiles alone leave CUs idle (aim for >= kSplitTarget
+// workgroups), but only rows of >= kSplitMinPairs block pairs, and keep >=
+// kSplitPairs per split: a split's fixed costs (pipeline fill, the store of
+// its partial tile, the reduce launch) outweigh the extra workgroups on
+// shorter ones.  Measured (whole call): K=2048, N=8192, M=65 / 128 / 192:
+// 20.4 / 23.1 / 28.1 -> 15.1 / 16.0 / 19.6 us unsplit (the former rule split
+// down to 8 pairs); M=512, K=1536, N=2560 25.5 -> 17.2 us; K=8192, N=1536,
+// M=65 / 128: 20.9 / 23.3 -> 19.1 / 20.6 us with >= 16 pairs per split.
 template <int WN, int WM, int TN, int TM>
 int splits_for_tiles(long tiles, size_t pp) {
-  // Split K when the tiles alone leave CUs idle: aim for >= kSplitTarget
-  // workgroups while keeping >= 8 block pairs per split.
   int splits = 1;
-  while (tiles * splits < kSplitTarget && pp / (2 * splits) >= 8) splits *= 2;
+  if (pp < kSplitMinPairs) return splits;
+  while (tiles * splits < kSplitTarget && pp / (2 * splits) >= kSplitPairs) splits *= 2;
   return splits;
 }
 

@@ -51,7 +51,8 @@ def _hidden(k, tokens, seed):
 @pytest.mark.parametrize("per_row", [False, True])
 @pytest.mark.parametrize("norm", [True, False])
 # tokens: the one-launch GEMV, the M <= 4 batch kernel, the matrix-core batch kernel on one shared
-# activation image, the GEMM over all matrices in one launch (one split-K reduce).
+# activation image, the GEMM over all matrices in one launch (at K=4096 with K split 4 ways and
+# one split-K reduce over all matrices).
 @pytest.mark.parametrize("tokens", [1, 3, 16, 100])
 @pytest.mark.parametrize("k,rows", BLOCKS)
 def test_norm_gemv_matches_oracle_and_op_sequence(gpu_ctx, oracle, k, rows, tokens, norm, per_row):
