@@ -496,9 +496,23 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
   }
   if (int r = set_device(ctx)) return r;
   // Small batches are weight-stream bound: nibble planes, no operand image.
-  if (lgh::plan_q4_batch(m, bpr).ok) {  // m <= 4: x quantized inside the kernel, dot4
-    for (int j = 0; j < nmat; j++)
-      LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w[j], x_dev, y_dev[j], m, mode, ctx->act_mode, ctx->stream));
+  if (lgh::plan_q4_batch(m, bpr).ok) {  // m <= 4: dot4 on the nibble planes
+    if (lgh::q4_batch_quantize_once(bpr)) {  // long rows: x quantized once, shared by every matrix
+      Carve cv;
+      const size_t oq = cv.take(m * k), os = cv.take(m * bpr * sizeof(float)), orow = cv.take(m * sizeof(float));
+      if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
+      char *ws = static_cast<char *>(ctx->ws);
+      auto *qs = reinterpret_cast<int8_t *>(ws + oq);
+      auto *sc = reinterpret_cast<float *>(ws + os);
+      LGH_HIP(ctx, lgh::launch_act_quant(x_dev, m, k, ctx->act_mode, qs, sc, nullptr,
+                                         reinterpret_cast<float *>(ws + orow), ctx->stream));
+      for (int j = 0; j < nmat; j++)
+        LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w[j], nullptr, qs, sc, y_dev[j], m, mode, 0, ctx->stream));
+      return LGH_OK;
+    }
+    for (int j = 0; j < nmat; j++)  // x quantized inside the kernel
+      LGH_HIP(ctx, lgh::launch_q4_gemv_batch(w[j], x_dev, nullptr, nullptr, y_dev[j], m, mode, ctx->act_mode,
+                                             ctx->stream));
     return LGH_OK;
   }
   if (lgh::plan_q4_mma(nmax, m, bpr).ok) {  // m <= 64: activation image, then int8 MFMA per block

@@ -240,17 +240,23 @@ hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
 struct Q4BatchArgs {
   const uint8_t *qs;
   const uint16_t *sc;
-  const float *x;  // f32 [m][k]
-  float *y;        // [m][n]
+  const float *x;    // f32 [m][k]
+  const int8_t *aq;  // PREQ: ActQ8 codes [m][k] and scales [m][k/32] instead of x
+  const float *as;
+  float *y;  // [m][n]
   int n, bpr, m, mode, per_row;
 };
 
-template <int T, int BPL, int KW, int W>
+// PREQ: the T rows arrive already quantized (act_quant_kernel, once for
+// every workgroup) instead of each workgroup quantizing all of them.
+template <int T, int BPL, int KW, int W, bool PREQ>
 __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;
   constexpr int RG = W / KW;
-  constexpr int XJ = (KB * 8 + THREADS - 1) / THREADS;
+  constexpr int XJ = PREQ ? 1 : (KB * 8 + THREADS - 1) / THREADS;
+  constexpr int QJ = PREQ ? (KB * 2 + THREADS - 1) / THREADS : 1;  // 16-byte code chunks per thread and row
+  constexpr int SJ = PREQ ? (KB + THREADS - 1) / THREADS : 1;      // block scales per thread and row
   static_assert(W % KW == 0, "slices divide the waves");
   __shared__ __align__(16) int8_t s_qs[T][KB * 32];
   __shared__ float s_sa[T][KB];
@@ -266,14 +272,27 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
   const int r = lane >> 4, c = lane & 15;
   const int kb0 = ks * 16 * BPL + c;
 
-  // (1) the x rows (tokens >= m read as 0), issued before the weights so
-  // that waiting for them leaves the weight loads in flight.
+  // (1) the x rows -- or (PREQ) their codes and block scales -- (tokens >= m
+  // read as 0), issued before the weights so that waiting for them leaves the
+  // weight loads in flight.
   float4 xv[T][XJ];
+  uint4 qv[T][QJ];
+  float sv[T][SJ];
 #pragma unroll
   for (int t = 0; t < T; t++) {
-    const auto xr = make_rsrc(a.x + static_cast<size_t>(t) * bpr * 32, t < a.m ? static_cast<uint32_t>(bpr) * 128u : 0u);
+    if constexpr (PREQ) {
+      const auto qr = make_rsrc(a.aq + static_cast<size_t>(t) * bpr * 32, t < a.m ? static_cast<uint32_t>(bpr) * 32u : 0u);
+      const auto ar = make_rsrc(a.as + static_cast<size_t>(t) * bpr, t < a.m ? static_cast<uint32_t>(bpr) * 4u : 0u);
 #pragma unroll
-    for (int j = 0; j < XJ; j++) xv[t][j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+      for (int j = 0; j < QJ; j++) qv[t][j] = buf_load16(qr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+#pragma unroll
+      for (int j = 0; j < SJ; j++) sv[t][j] = buf_load_f32(ar, static_cast<uint32_t>(tid + j * THREADS) * 4u);
+    } else {
+      const auto xr =
+          make_rsrc(a.x + static_cast<size_t>(t) * bpr * 32, t < a.m ? static_cast<uint32_t>(bpr) * 128u : 0u);
+#pragma unroll
+      for (int j = 0; j < XJ; j++) xv[t][j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
+    }
   }
 
   // (2) every weight load of this lane (rows past n read as 0).
@@ -291,10 +310,27 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
   }
 
   // (3) codes into LDS.
+  if constexpr (PREQ) {
 #pragma unroll
-  for (int t = 0; t < T; t++) {
-    const float rs = row_scale_of<THREADS, XJ>(xv[t], a.per_row, s_red);
-    quant_regs<THREADS, XJ>(xv[t], bpr, a.per_row != 0, rs, s_qs[t], s_sa[t]);
+    for (int t = 0; t < T; t++) {
+#pragma unroll
+      for (int j = 0; j < QJ; j++) {
+        const int i = tid + j * THREADS;
+        if (i < KB * 2) reinterpret_cast<uint4 *>(s_qs[t])[i] = qv[t][j];
+      }
+#pragma unroll
+      for (int j = 0; j < SJ; j++) {
+        const int i = tid + j * THREADS;
+        if (i < KB) s_sa[t][i] = sv[t][j];
+      }
+    }
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const float rs = row_scale_of<THREADS, XJ>(xv[t], a.per_row, s_red);
+      quant_regs<THREADS, XJ>(xv[t], bpr, a.per_row != 0, rs, s_qs[t], s_sa[t]);
+    }
   }
 
   // (4) per block: one unpack, then T dots and folds.
@@ -355,12 +391,12 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
   }
 }
 
-template <int BPL, int KW>
+template <int BPL, int KW, bool PREQ = false>
 hipError_t launch_batch(const Q4BatchArgs &a, hipStream_t st) {
   constexpr int W = 8;
   const int rows_per_wg = 4 * W / KW;
   const unsigned wgs = static_cast<unsigned>((a.n + rows_per_wg - 1) / rows_per_wg);
-  hipLaunchKernelGGL((q4_gemv_batch_kernel<4, BPL, KW, W>), dim3(wgs), dim3(W * kWave), 0, st, a);
+  hipLaunchKernelGGL((q4_gemv_batch_kernel<4, BPL, KW, W, PREQ>), dim3(wgs), dim3(W * kWave), 0, st, a);
   return hipGetLastError();
 }
 
@@ -894,13 +930,25 @@ Q4BatchPlan plan_q4_batch(size_t m, size_t bpr) {
   return p;
 }
 
-hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, float *y, size_t m, int mode, int per_row,
-                                hipStream_t st) {
+// Rows of more than 64 blocks (two or four K slices per row group) are
+// quantized once by act_quant_kernel: inside the kernel every workgroup would
+// quantize all m rows, m * k elements (256 workgroups at K=8192, N=2048).
+// Measured, whole call: K=8192, N=2048, M=2 / 4 9.47 / 10.05 -> 7.35 /
+// 7.42 us; K=4096, N=8192 9.41 / 10.19 -> 8.70 / 8.98 us; K=3072, N=8192
+// 8.25 / 8.90 -> 8.04 / 8.37 us.
+bool q4_batch_quantize_once(size_t bpr) { return bpr > 64; }
+
+hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *codes, const float *scales, float *y,
+                                size_t m, int mode, int per_row, hipStream_t st) {
   const Q4BatchPlan p = plan_q4_batch(m, w->bpr);
   if (!p.ok) return hipErrorInvalidValue;
   if (w->n == 0) return hipSuccess;
-  Q4BatchArgs a{w->qs, w->sc, x, y, static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(m), mode,
-                per_row};
+  Q4BatchArgs a{w->qs,  w->sc, x, codes, scales, y, static_cast<int>(w->n), static_cast<int>(w->bpr),
+                static_cast<int>(m), mode, per_row};
+  if (codes) {
+    if (p.KW == 1) return hipErrorInvalidValue;
+    return p.KW == 2 ? launch_batch<4, 2, true>(a, st) : launch_batch<4, 4, true>(a, st);
+  }
   if (p.KW == 1) {
     switch (p.BPL) {
       case 1: return launch_batch<1, 1>(a, st);

@@ -155,8 +155,12 @@ struct Q4BatchPlan {
   bool ok;
 };
 Q4BatchPlan plan_q4_batch(size_t m, size_t bpr);
-hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, float *y, size_t m, int mode, int per_row,
-                                hipStream_t stream);
+// Rows of > 64 blocks are quantized once (act_quant_kernel) and the kernel
+// reads the codes: inside it, every workgroup would quantize all m rows.
+bool q4_batch_quantize_once(size_t bpr);
+// codes / scales (ActQ8 of the m rows, [m][k] and [m][k/32]) replace x when non-null.
+hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *codes, const float *scales, float *y,
+                                size_t m, int mode, int per_row, hipStream_t stream);
 // Batched GEMV on the matrix cores for 2 <= m <= 64 (TT 16-token tiles, KW
 // K slices, CB-block chunks, RG 16-row groups per workgroup) on an
 // activation image written by act_quant_mma, with mt = ceil(m/16) token

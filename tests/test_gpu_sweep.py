@@ -79,3 +79,16 @@ def test_gemm_five_wave_route_three_matrices(gpu_ctx, oracle):
     for j, (o, n, b) in enumerate(zip(outs, rows, bl)):
         ref = oracle.gemm_q4(oracle.Q4Matrix(n, k, b), x, tokens, kernel=oracle.KERNEL_SCALAR, threads=8)
         assert_close(o, ref.ravel(), what=f"matrix {j}")
+
+
+# M = 2..4 with rows of 65..256 blocks (K = 2080..8192): x is quantized once by the ActQ8 kernel
+# and the batched GEMV reads the codes (ragged N, odd block counts).
+BATCH_LONG = [(2, 1536, 8192), (3, 1000, 4096), (4, 2048, 8192), (4, 33, 6144), (2, 130, 4128),
+              (3, 700, 3072), (4, 96, 2080)]
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("m,n,k", BATCH_LONG)
+def test_batch_long_rows(gpu_ctx, oracle, m, n, k, mode, per_row):
+    test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 7 * m + n + k + mode)
