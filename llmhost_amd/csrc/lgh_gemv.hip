@@ -962,17 +962,16 @@ hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *c
 
 // Token tiles TT = ceil(m / 16) (<= 4); 8-block chunks; KW (a power of
 // two <= 8) K slices per 16 rows: one chunk per wave for one or two token
-// tiles, two for four (measured at N=8192, K=2048: more, smaller waves are
+// tiles, two for three or four (measured at N=8192, K=2048: more, smaller waves are
 // faster while a chunk's registers stay small, then occupancy wins); RG row
 // groups make the workgroup at least 4 waves.
 Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr) {
   Q4MmaPlan p{};
   if (m < 2 || m > 64 || bpr == 0 || n == 0) return p;
   p.TT = static_cast<int>((m + 15) / 16);
-  if (p.TT == 3) p.TT = 4;
   p.CB = 8;
   const size_t nch = (bpr + p.CB - 1) / p.CB;
-  const size_t per_wave = p.TT == 4 ? 2 : 1;
+  const size_t per_wave = p.TT >= 3 ? 2 : 1;
   p.KW = 1;
   while (p.KW < 8 && static_cast<size_t>(p.KW) * per_wave < nch) p.KW *= 2;
   p.RG = p.KW >= 4 ? 1 : 4 / p.KW;
@@ -996,6 +995,10 @@ hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float
   LGH_M(2, 2, 8, 2);
   LGH_M(2, 4, 8, 1);
   LGH_M(2, 8, 8, 1);
+  LGH_M(3, 1, 8, 4);
+  LGH_M(3, 2, 8, 2);
+  LGH_M(3, 4, 8, 1);
+  LGH_M(3, 8, 8, 1);
   LGH_M(4, 1, 8, 4);
   LGH_M(4, 2, 8, 2);
   LGH_M(4, 4, 8, 1);
