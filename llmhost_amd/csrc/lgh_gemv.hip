@@ -968,6 +968,11 @@ hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *c
 Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr) {
   Q4MmaPlan p{};
   if (m < 2 || m > 64 || bpr == 0 || n == 0) return p;
+  // Four token tiles over long rows: the fp6 GEMM is faster (M=64, whole
+  // call: K=8192, N=1536 / 2048 / 8192 20.4 / 20.7 / 36.6 -> 18.5 / 19.3 /
+  // 29.8 us; K=4096, N=16384 39.1 -> 30.9 us), but not where its grid is
+  // small (K=4096, N=4096: 13.7 us here, 18.0 us on the GEMM).
+  if (m > 48 && (bpr >= 256 || (bpr >= 128 && n >= 16384))) return p;
   p.TT = static_cast<int>((m + 15) / 16);
   p.CB = 8;
   const size_t nch = (bpr + p.CB - 1) / p.CB;

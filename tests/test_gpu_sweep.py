@@ -92,3 +92,15 @@ BATCH_LONG = [(2, 1536, 8192), (3, 1000, 4096), (4, 2048, 8192), (4, 33, 6144), 
 @pytest.mark.parametrize("m,n,k", BATCH_LONG)
 def test_batch_long_rows(gpu_ctx, oracle, m, n, k, mode, per_row):
     test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 7 * m + n + k + mode)
+
+
+# M = 49..64 over long rows (K >= 8192, or K >= 4096 with N >= 16384) takes the fp6 GEMM instead
+# of the four-token-tile MMA kernel; M = 48 and K = 4096 with N = 4096 stay on the MMA kernel.
+LONG_ROWS = [(64, 1536, 8192), (49, 300, 8224), (56, 16384, 4096), (48, 1536, 8192), (64, 4096, 4096)]
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("m,n,k", LONG_ROWS)
+def test_long_rows_route(gpu_ctx, oracle, m, n, k, mode, per_row):
+    test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 11 * m + n + k + mode)
