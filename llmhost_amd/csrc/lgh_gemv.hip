@@ -785,8 +785,9 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
   while (p.W > 4 && p.W > p.KW && n * nmat / static_cast<size_t>(4 * p.W / p.KW) < 192) p.W >>= 1;
   // Long rows: twice the blocks per lane and half the slices (twice the rows
   // per workgroup, half the workgroups re-quantizing x) while >= 512
-  // workgroups remain (K=8192: N=16384 19.9 -> 14.9 us, N=4096 6.4 -> 5.5 us).
-  while (p.W == 16 && p.KW >= 8 && p.BPL < 4 && n * nmat * static_cast<size_t>(p.KW / 2) / 64 >= 512) {
+  // workgroups remain (K=8192: N=16384 19.9 -> 14.9 us, N=4096 6.4 -> 5.5 us;
+  // K=4096: N=16384 9.4 -> 8.3 us, N=32768 16.4 -> 14.4 us).
+  while (p.W == 16 && p.KW >= 4 && p.BPL < 4 && n * nmat * static_cast<size_t>(p.KW / 2) / 64 >= 512) {
     p.KW /= 2;
     p.BPL *= 2;
   }
@@ -809,7 +810,9 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
 
 // Quantize x once (act_quant_kernel) and run the codes GEMV instead when
 // the workgroups would re-quantize more than ~12M elements of x between them
-// (K=16384, N=8192: 19.5 -> 15.9 us; K=8192, N=16384 is even at 8.4M).
+// (K=16384, N=8192: 19.5 -> 15.9 us; K=8192, N=16384 is even at 8.4M; a 4M
+// threshold was slower at K=4096, N=16384 (9.4 -> 10.7 us) and K=8192,
+// N=4096 (5.6 -> 7.5 us): the extra launch costs more).
 bool q4_gemv_quantize_once(size_t n, size_t bpr, int nmat) {
   const Q4GemvPlan p = plan_q4_gemv(n, bpr, nmat);
   return p.ok && static_cast<size_t>(p.wgs_per_mat) * nmat * bpr * 32 >= (size_t{12} << 20);
@@ -904,6 +907,7 @@ hipError_t launch_q4_gemv_multi(const lgh_q4 *const *w, float *const *y, int nma
   LGH_G16(2, 8, 8);
   LGH_G16(2, 16, 16);
   LGH_G16(4, 16, 16);
+  LGH_G16(4, 2, 16);
   LGH_G16(4, 4, 16);
   LGH_G16(4, 8, 16);
 #undef LGH_G16

@@ -104,3 +104,22 @@ LONG_ROWS = [(64, 1536, 8192), (49, 300, 8224), (56, 16384, 4096), (48, 1536, 81
 @pytest.mark.parametrize("m,n,k", LONG_ROWS)
 def test_long_rows_route(gpu_ctx, oracle, m, n, k, mode, per_row):
     test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 11 * m + n + k + mode)
+
+
+# M = 1 over rows of 65..128 blocks at N*matrices >= 16384: the GEMV takes 4 blocks per lane and
+# 2 K slices (32 rows per workgroup); also for the gate/up pair.
+@pytest.mark.parametrize("n,k", [(16384, 4096), (20000, 3072), (16400, 2080)])
+def test_gemv_long_rows_wide(gpu_ctx, oracle, n, k):
+    test_gemm_sweep(gpu_ctx, oracle, 1, n, k, 0, False, n + k)
+
+
+def test_gemv_pair_long_rows(gpu_ctx, oracle):
+    n, k = 8192, 4096
+    bg, bu = synth.q4_blocks(71, n, k), synth.q4_blocks(72, n, k)
+    wg = q4.Q4Matrix.from_blocks(n, k, bg, gpu_ctx)
+    wu = q4.Q4Matrix.from_blocks(n, k, bu, gpu_ctx)
+    x = synth.normal_f32(73, k)
+    og, ou = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    q4.gemv_q4_pair(wg, wu, x, og, ou)
+    assert_close(og, oracle.gemv_q4(oracle.Q4Matrix(n, k, bg), x, kernel=oracle.KERNEL_SCALAR, threads=8), what="gate")
+    assert_close(ou, oracle.gemv_q4(oracle.Q4Matrix(n, k, bu), x, kernel=oracle.KERNEL_SCALAR, threads=8), what="up")
