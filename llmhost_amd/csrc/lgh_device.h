@@ -521,12 +521,11 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-// Read one MFMA operand row (6 dwords) from a 768-byte tile image (LDS or
-// global): plane0 at tile + off16, plane1 at tile + 512 + off8 (row * 16 and
-// row * 8).
-__device__ __forceinline__ v8i mx_row_at(const char *tile, int off16, int off8) {
-  const uint4 p0 = *reinterpret_cast<const uint4 *>(tile + off16);
-  const uint2 p1 = *reinterpret_cast<const uint2 *>(tile + 512 + off8);
+// One MFMA operand row (6 dwords): 16 bytes of plane0 at p16, 8 bytes of
+// plane1 at p8.
+__device__ __forceinline__ v8i mx_operand(const char *p16, const char *p8) {
+  const uint4 p0 = *reinterpret_cast<const uint4 *>(p16);
+  const uint2 p1 = *reinterpret_cast<const uint2 *>(p8);
   v8i r;
   r[0] = static_cast<int>(p0.x);
   r[1] = static_cast<int>(p0.y);
@@ -539,7 +538,11 @@ __device__ __forceinline__ v8i mx_row_at(const char *tile, int off16, int off8) 
   return r;
 }
 
-__device__ __forceinline__ v8i mx_row(const char *tile, int row) { return mx_row_at(tile, row * 16, row * 8); }
+// Row `row` of a 768-byte tile image (LDS or global): plane0 at tile + row * 16,
+// plane1 at tile + 512 + row * 8.
+__device__ __forceinline__ v8i mx_row(const char *tile, int row) {
+  return mx_operand(tile + row * 16, tile + 512 + row * 8);
+}
 
 // The same value, opaque to the optimizer (no instruction): addresses built
 // from it are not merged with addresses built from the original.

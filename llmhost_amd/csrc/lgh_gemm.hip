@@ -188,21 +188,6 @@ __device__ __forceinline__ StageOffs stage_offsets(int wn, int wm) {
   return o;
 }
 
-__device__ __forceinline__ v8i mx_operand(const char *p16, const char *p8) {
-  const uint4 p0 = *reinterpret_cast<const uint4 *>(p16);
-  const uint2 p1 = *reinterpret_cast<const uint2 *>(p8);
-  v8i r;
-  r[0] = static_cast<int>(p0.x);
-  r[1] = static_cast<int>(p0.y);
-  r[2] = static_cast<int>(p0.z);
-  r[3] = static_cast<int>(p0.w);
-  r[4] = static_cast<int>(p1.x);
-  r[5] = static_cast<int>(p1.y);
-  r[6] = 0;
-  r[7] = 0;
-  return r;
-}
-
 // One stage of the inner loop for a wave's TN x TM tiles: per tile, the
 // outer product of the two blocks' scales, the two blocks' exact dots, and
 // 32 FMAs folding them into the accumulators (block order as in the reference).
