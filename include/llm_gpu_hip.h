@@ -42,6 +42,8 @@ extern "C" {
 #define LGH_ERR_ARCH (-4)        /* device is not gfx950                       */
 #define LGH_ERR_NO_DEVICE (-5)   /* no such HIP device                         */
 #define LGH_ERR_OOM (-6)         /* device or host allocation failed           */
+#define LGH_ERR_CAPTURE (-7)     /* a workspace would have to grow while the
+                                    context stream is being captured           */
 
 /* Accumulation mode, crates/llm-cpu/src/gemv_q4.rs:445-449 AccMode, plus the
  * f32 residual add the attention and conv blocks apply after their output
@@ -88,6 +90,13 @@ int lgh_set_stream(lgh_ctx *ctx, void *hip_stream);
 void *lgh_get_stream(const lgh_ctx *ctx);
 /* Wait for all work enqueued on the context stream. */
 int lgh_sync(lgh_ctx *ctx);
+/* Wait for the context stream, then release the context's grow-only device
+ * buffers (GEMM workspace, host-call staging, FFN intermediates); they grow
+ * again on the next call that needs them.  Workspaces grow only outside
+ * stream capture: a call under capture that would grow one returns
+ * LGH_ERR_CAPTURE, so run each shape once before capturing.  No reference
+ * counterpart (llm-cpu keeps no device buffers). */
+int lgh_trim(lgh_ctx *ctx);
 
 /* ---- weights ------------------------------------------------------------
  * Q4Matrix::from_blocks (crates/llm-cpu/src/gemv_q4.rs:128-149): upload
@@ -103,6 +112,18 @@ int lgh_q4_upload_dev(lgh_ctx *ctx, const void *blocks_dev, size_t n, size_t k, 
 int lgh_q4_from_f32(lgh_ctx *ctx, const float *w, size_t n, size_t k, lgh_q4 **out);
 /* Copy the device matrix back as BlockQ4[n][k/32] (18-byte blocks). */
 int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks);
+/* Build the matrix's GEMM operand image now (28 B per 32 weights, fp6 codes
+ * and f32 scales in the matrix-core layout).  An upload holds only the
+ * 18 B/32 nibble and scale planes; the first call that routes the matrix to
+ * the GEMM (m >= 65, long rows at m >= 49, or k > 32768) builds the image
+ * itself, which allocates -- so call this before capturing such a call in a
+ * graph.  LGH_ERR_SHAPE if
+ * the image would exceed 2 GiB.  No reference counterpart: llm-cpu's Q4Matrix
+ * packs its tiles (and AMX panels) at load, gemv_q4.rs:116-209. */
+int lgh_q4_prepare_gemm(lgh_ctx *ctx, const lgh_q4 *w);
+/* Device bytes the matrix holds: the nibble and scale planes, plus the GEMM
+ * image once built. */
+size_t lgh_q4_device_bytes(const lgh_q4 *w);
 void lgh_q4_free(lgh_q4 *w);
 size_t lgh_q4_rows(const lgh_q4 *w);
 size_t lgh_q4_cols(const lgh_q4 *w);
@@ -236,6 +257,11 @@ int lgh_q4_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t 
  * consumes them (hq, hs may be NULL).  hidden is not modified. */
 int lgh_q4_ffn_gate_up(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const float *norm_w, float eps,
                        const float *hidden, float *g, float *u, float *h, int8_t *hq, float *hs);
+/* Host-only check of the kernel dispatch (no device needed): the number of
+ * GEMV launch shapes the planner can choose, over a sweep of row counts
+ * around every planner threshold, every K up to 32768 and 1-3 matrices, that
+ * have no compiled Q4 / Q8_0 kernel.  0 means every plan can launch. */
+int lgh_gemv_plans_uncovered(void);
 /* Integer Q8_0 x Q8 block dot (crates/llm-engine/src/weights.rs:206-209). */
 int lgh_q8_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks,
                       int32_t *out);

@@ -20,6 +20,7 @@ LGH_ERR_HIP = -3
 LGH_ERR_ARCH = -4
 LGH_ERR_NO_DEVICE = -5
 LGH_ERR_OOM = -6
+LGH_ERR_CAPTURE = -7
 
 LGH_ASSIGN = 0
 LGH_ADD_F64 = 1
@@ -42,10 +43,13 @@ SIGNATURES = {
     "lgh_set_stream": (_I, [_P, _P]),
     "lgh_get_stream": (_P, [_P]),
     "lgh_sync": (_I, [_P]),
+    "lgh_trim": (_I, [_P]),
     "lgh_q4_upload": (_I, [_P, _P, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_upload_dev": (_I, [_P, _P, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_from_f32": (_I, [_P, _P, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_download": (_I, [_P, _P, _P]),
+    "lgh_q4_prepare_gemm": (_I, [_P, _P]),
+    "lgh_q4_device_bytes": (_SZ, [_P]),
     "lgh_q4_free": (None, [_P]),
     "lgh_q4_rows": (_SZ, [_P]),
     "lgh_q4_cols": (_SZ, [_P]),
@@ -69,6 +73,7 @@ SIGNATURES = {
     "lgh_q4_gemv_prep_dev": (_I, [_P, _P, _P, _P, _P, _I]),
     "lgh_q4_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_q8_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
+    "lgh_gemv_plans_uncovered": (_I, []),
     "lgh_q4_mfma_block_dots": (_I, [_P, _P, _P, _SZ, _P]),
     "lgh_rms_norm": (_I, [_P, _P, _P, _SZ, _SZ, C.c_float, _P]),
     "lgh_rms_norm_dev": (_I, [_P, _P, _P, _SZ, _SZ, C.c_float, _P]),

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "lgh_internal.h"
@@ -18,6 +19,7 @@
 namespace {
 
 thread_local std::string g_init_err;
+
 
 int fail(lgh_ctx *ctx, int code, const char *fmt, ...) {
   char buf[512];
@@ -51,8 +53,16 @@ int set_device(lgh_ctx *ctx) {
 }
 
 // Grow-only device buffer; waits for queued work before releasing the old one.
+// A stream under graph capture cannot synchronize or allocate: growing there
+// fails with LGH_ERR_CAPTURE (the caller warms the shape up eagerly first).
 int ensure(lgh_ctx *ctx, void **buf, size_t *cap, size_t bytes) {
   if (bytes <= *cap) return LGH_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(ctx, LGH_ERR_CAPTURE,
+                "a workspace must grow to %zu bytes while the stream is being captured; run the same "
+                "shape once before capturing",
+                bytes);
   if (*buf) {
     LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
     LGH_HIP(ctx, hipFree(*buf));
@@ -69,6 +79,21 @@ int ensure(lgh_ctx *ctx, void **buf, size_t *cap, size_t bytes) {
   return LGH_OK;
 }
 
+// Free a grow-only buffer (the caller has synchronized the stream).
+void release(lgh_ctx *, void **buf, size_t *cap) {
+  if (*buf) (void)hipFree(*buf);
+  *buf = nullptr;
+  *cap = 0;
+}
+
+// The host-call staging buffer keeps its peak size between calls; after a
+// weight upload that staged more than this (an fp32 matrix, e.g. 512 MB for a
+// 65536 x 2048 head) it is released once the upload has completed.
+constexpr size_t kStageKeepBytes = size_t(64) << 20;
+void trim_stage(lgh_ctx *ctx) {
+  if (ctx->stage_bytes > kStageKeepBytes) release(ctx, &ctx->stage, &ctx->stage_bytes);
+}
+
 // Carve consecutive 256-byte aligned regions out of the staging buffer.
 struct Carve {
   size_t off = 0;
@@ -81,6 +106,37 @@ struct Carve {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Where one call takes its device scratch (activation images, codes, split-K
+// partials): the context's grow-only workspace, or -- for the entry point that
+// allocates nothing -- the device's fixed scratch array, which a request larger
+// than its capacity cannot grow (LGH_ERR_SHAPE).
+struct Ws {
+  lgh_ctx *ctx;
+  char *fixed;  // non-null: the fixed scratch of ctx's device
+  size_t cap;   // its size in bytes
+  int get(size_t bytes, char **out) const {
+    if (fixed) {
+      if (bytes > cap)
+        return fail(ctx, LGH_ERR_SHAPE, "the call needs %zu bytes of scratch; the fixed scratch holds %zu", bytes,
+                    cap);
+      *out = fixed;
+      return LGH_OK;
+    }
+    if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, bytes)) return r;
+    *out = static_cast<char *>(ctx->ws);
+    return LGH_OK;
+  }
+  size_t limit() const { return fixed ? cap : SIZE_MAX; }
+};
+
+Ws grow_ws(lgh_ctx *ctx) { return Ws{ctx, nullptr, 0}; }
+
+void set_tiles(lgh_q8 *) {}
+void set_tiles(lgh_q4 *w) {
+  w->nt = (w->n + 31) / 32;
+  w->pp = (w->bpr + 1) / 2;
+}
+
 template <class M>
 int alloc_matrix(lgh_ctx *ctx, size_t n, size_t k, size_t qs_bytes_per_block, M **out) {
   auto *w = new (std::nothrow) M();
@@ -89,6 +145,7 @@ int alloc_matrix(lgh_ctx *ctx, size_t n, size_t k, size_t qs_bytes_per_block, M 
   w->n = n;
   w->k = k;
   w->bpr = k / 32;
+  set_tiles(w);
   const size_t nb = n * w->bpr;
   const size_t qs_bytes = align_up(nb * qs_bytes_per_block);
   const size_t bytes = qs_bytes + align_up(nb * 2);
@@ -124,21 +181,59 @@ void free_matrix(M *w) {
   delete w;
 }
 
-// GEMM operand image of a Q4 matrix, built from its nibble/scale planes.
-// Matrices whose image would not fit 31-bit buffer offsets keep mx = null;
-// the GEMV path serves them and the GEMM entry points report LGH_ERR_SHAPE.
-int build_mx(lgh_ctx *ctx, lgh_q4 *w) {
-  w->nt = (w->n + 31) / 32;
-  w->pp = (w->bpr + 1) / 2;
+// GEMM operand image of a Q4 matrix, built from its nibble/scale planes on
+// the first call that routes the matrix to the GEMM (or by
+// lgh_q4_prepare_gemm), so matrices that only ever serve decode GEMVs hold
+// their 18 B per 32 weights and nothing more.  The image is a function of the
+// immutable planes; the matrix's mutex makes the one-time build safe when
+// contexts on several threads share the matrix, and the build waits for its
+// pack kernel so every later user sees the finished image.  Matrices whose
+// image would not fit 31-bit buffer offsets have none: the GEMV path serves
+// them and the GEMM routes report LGH_ERR_SHAPE.
+bool mx_fits(const lgh_q4 *w) {
+  const size_t nt = (w->n + 31) / 32, pp = (w->bpr + 1) / 2;
+  return nt * pp > 0 && (nt + 8) * pp * lgh::kMxWRec < lgh::kMxMaxBytes;
+}
+
+bool has_mx(const lgh_q4 *wc) {
+  auto *w = const_cast<lgh_q4 *>(wc);
+  std::lock_guard<std::mutex> lock(w->mx_mu);
+  return w->mx != nullptr;
+}
+
+int ensure_mx(lgh_ctx *ctx, const lgh_q4 *wc) {
+  auto *w = const_cast<lgh_q4 *>(wc);
+  std::lock_guard<std::mutex> lock(w->mx_mu);
+  if (w->mx) return LGH_OK;
+  if (!mx_fits(w)) return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w->n, w->k);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(ctx, LGH_ERR_CAPTURE,
+                "the %zu x %zu matrix has no GEMM image yet and it cannot be built under stream capture; call "
+                "lgh_q4_prepare_gemm first",
+                w->n, w->k);
   const size_t bytes = w->nt * w->pp * lgh::kMxWRec;
-  if (!bytes || (w->nt + 8) * w->pp * lgh::kMxWRec >= lgh::kMxMaxBytes) return LGH_OK;
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess)
     return fail(ctx, LGH_ERR_OOM, "hipMalloc(%zu bytes) for the GEMM operand image failed: %s", bytes,
                 hipGetErrorString(e));
+  lgh_q4 tmp;  // the pack launcher reads the shape and the destination from a matrix
+  tmp.n = w->n;
+  tmp.k = w->k;
+  tmp.bpr = w->bpr;
+  tmp.qs = w->qs;
+  tmp.sc = w->sc;
+  tmp.nt = w->nt;
+  tmp.pp = w->pp;
+  tmp.mx = static_cast<uint8_t *>(p);
+  e = lgh::launch_q4_mx_pack(&tmp, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(ctx, e, "GEMM image pack");
+  }
   w->mx = static_cast<uint8_t *>(p);
-  LGH_HIP(ctx, lgh::launch_q4_mx_pack(w, ctx->stream));
   return LGH_OK;
 }
 
@@ -227,19 +322,26 @@ int lgh_sync(lgh_ctx *ctx) {
   return LGH_OK;
 }
 
+int lgh_trim(lgh_ctx *ctx) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  release(ctx, &ctx->ws, &ctx->ws_bytes);
+  release(ctx, &ctx->stage, &ctx->stage_bytes);
+  release(ctx, &ctx->ffn, &ctx->ffn_bytes);
+  return LGH_OK;
+}
+
 // ---- weights -------------------------------------------------------------
 namespace {
-// Build the GEMM image of a freshly repacked matrix and wait for the upload.
+// Wait for the repack of a fresh matrix (the GEMM image is built on first use).
 int finish_q4(lgh_ctx *ctx, lgh_q4 *w, lgh_q4 **out) {
-  int r = build_mx(ctx, w);
-  if (r == LGH_OK) {
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) r = hip_fail(ctx, e, "Q4 upload");
-  }
-  if (r != LGH_OK) {
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
     free_matrix(w);
-    return r;
+    return hip_fail(ctx, e, "Q4 upload");
   }
+  trim_stage(ctx);
   *out = w;
   return LGH_OK;
 }
@@ -298,6 +400,20 @@ int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks) {
   return LGH_OK;
 }
 
+int lgh_q4_prepare_gemm(lgh_ctx *ctx, const lgh_q4 *w) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (w->n == 0 || w->bpr == 0) return LGH_OK;
+  if (int r = set_device(ctx)) return r;
+  return ensure_mx(ctx, w);
+}
+
+size_t lgh_q4_device_bytes(const lgh_q4 *w) {
+  if (!w) return 0;
+  const size_t nb = w->n * w->bpr;
+  return align_up(nb * 16) + align_up(nb * 2) + (has_mx(w) ? w->nt * w->pp * lgh::kMxWRec : 0);
+}
+
 void lgh_q4_free(lgh_q4 *w) { free_matrix(w); }
 size_t lgh_q4_rows(const lgh_q4 *w) { return w ? w->n : 0; }
 size_t lgh_q4_cols(const lgh_q4 *w) { return w ? w->k : 0; }
@@ -317,6 +433,7 @@ int lgh_q8_upload(lgh_ctx *ctx, const void *blocks, size_t n, size_t k, lgh_q8 *
     free_matrix(w);
     return hip_fail(ctx, e, "Q8 upload");
   }
+  trim_stage(ctx);
   *out = w;
   return LGH_OK;
 }
@@ -336,6 +453,7 @@ int lgh_q8_from_f32(lgh_ctx *ctx, const float *wf, size_t n, size_t k, lgh_q8 **
     free_matrix(w);
     return hip_fail(ctx, e, "Q8 quantize");
   }
+  trim_stage(ctx);
   *out = w;
   return LGH_OK;
 }
@@ -364,21 +482,22 @@ static int check_mode(lgh_ctx *ctx, int mode) {
   return LGH_OK;
 }
 
-int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode);
+static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
+                          float *const *y_dev, size_t m, int mode);
 
-static int launch_gemv(lgh_ctx *ctx, const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
-                       int mode) {
+static int launch_gemv(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1,
+                       const float *x, int mode) {
   if (!lgh::plan_q4_gemv(w0->n, w0->bpr, w1 ? 2 : 1).ok) {
     // K longer than the GEMV covers: batched act-quant + GEMM with m = 1.
-    if (int r = lgh_q4_gemm_dev(ctx, w0, x, y0, 1, mode)) return r;
-    return w1 ? lgh_q4_gemm_dev(ctx, w1, x, y1, 1, mode) : LGH_OK;
+    if (int r = gemm_multi_dev(ctx, wsp, &w0, 1, x, &y0, 1, mode)) return r;
+    return w1 ? gemm_multi_dev(ctx, wsp, &w1, 1, x, &y1, 1, mode) : LGH_OK;
   }
   if (int r = set_device(ctx)) return r;
   if (lgh::q4_gemv_quantize_once(w0->n, w0->bpr, w1 ? 2 : 1)) {
     Carve cv;
     const size_t oq = cv.take(w0->k), os = cv.take(w0->bpr * sizeof(float)), orow = cv.take(sizeof(float));
-    if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
-    char *ws = static_cast<char *>(ctx->ws);
+    char *ws = nullptr;
+    if (int r = wsp.get(cv.off, &ws)) return r;
     auto *qs = reinterpret_cast<int8_t *>(ws + oq);
     auto *sc = reinterpret_cast<float *>(ws + os);
     LGH_HIP(ctx, lgh::launch_act_quant(x, 1, w0->k, ctx->act_mode, qs, sc, nullptr,
@@ -397,7 +516,7 @@ int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  return launch_gemv(ctx, w, y_dev, nullptr, nullptr, x_dev, mode);
+  return launch_gemv(ctx, grow_ws(ctx), w, y_dev, nullptr, nullptr, x_dev, mode);
 }
 
 int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const float *x_dev, float *yg_dev,
@@ -410,7 +529,7 @@ int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const
   if (wg->n == 0) return LGH_OK;
   if (!yg_dev || !yu_dev || (wg->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  return launch_gemv(ctx, wg, yg_dev, wu, yu_dev, x_dev, LGH_ASSIGN);
+  return launch_gemv(ctx, grow_ws(ctx), wg, yg_dev, wu, yu_dev, x_dev, LGH_ASSIGN);
 }
 
 // gemv_q4_prep / gemv_q4_prep_add: the GEMV kernel reads ActQ8 codes and
@@ -481,8 +600,8 @@ int lgh_act_quant_dev(lgh_ctx *ctx, const float *x_dev, size_t m, size_t k, int8
 // activation quantization of each route (the MMA image, the GEMM's operand
 // image) is done once and read by every matrix.  m == 1 and m <= 4 quantize
 // inside their kernels, per matrix.
-static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const float *x_dev, float *const *y_dev,
-                          size_t m, int mode) {
+static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
+                          float *const *y_dev, size_t m, int mode) {
   const size_t k = w[0]->k, bpr = w[0]->bpr;
   size_t nmax = 0;
   for (int j = 0; j < nmat; j++) nmax = std::max(nmax, w[j]->n);
@@ -491,7 +610,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
   if (m == 1 && lgh::plan_q4_gemv(nmax, bpr, 1).ok) {
     for (int j = 0; j < nmat; j++)
       if (w[j]->n)
-        if (int r = launch_gemv(ctx, w[j], y_dev[j], nullptr, nullptr, x_dev, mode)) return r;
+        if (int r = launch_gemv(ctx, wsp, w[j], y_dev[j], nullptr, nullptr, x_dev, mode)) return r;
     return LGH_OK;
   }
   if (int r = set_device(ctx)) return r;
@@ -500,8 +619,8 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
     if (lgh::q4_batch_quantize_once(bpr)) {  // long rows: x quantized once, shared by every matrix
       Carve cv;
       const size_t oq = cv.take(m * k), os = cv.take(m * bpr * sizeof(float)), orow = cv.take(m * sizeof(float));
-      if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
-      char *ws = static_cast<char *>(ctx->ws);
+      char *ws = nullptr;
+      if (int r = wsp.get(cv.off, &ws)) return r;
       auto *qs = reinterpret_cast<int8_t *>(ws + oq);
       auto *sc = reinterpret_cast<float *>(ws + os);
       LGH_HIP(ctx, lgh::launch_act_quant(x_dev, m, k, ctx->act_mode, qs, sc, nullptr,
@@ -520,8 +639,8 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
     Carve cv;
     const size_t o_ci = cv.take(mt * pq * 2 * 1024), o_si = cv.take(mt * pq * 256);
     const size_t o_rs = cv.take(m * sizeof(float));
-    if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
-    char *ws = static_cast<char *>(ctx->ws);
+    char *ws = nullptr;
+    if (int r = wsp.get(cv.off, &ws)) return r;
     auto *ci = reinterpret_cast<uint8_t *>(ws + o_ci);
     auto *si = reinterpret_cast<float *>(ws + o_si);
     LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev, m, k, ctx->act_mode, ci, si,
@@ -530,25 +649,50 @@ static int gemm_multi_dev(lgh_ctx *ctx, const lgh_q4 *const *w, int nmat, const 
       if (w[j]->n) LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w[j], ci, si, y_dev[j], m, mode, ctx->stream));
     return LGH_OK;
   }
-  for (int j = 0; j < nmat; j++)
-    if (w[j]->n && !w[j]->mx)
-      return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w[j]->n, w[j]->k);
-  // Tokens per launch: the activation image must fit 31-bit buffer offsets.
+  for (int j = 0; j < nmat; j++) {
+    if (!w[j]->n) continue;
+    if (wsp.fixed) {  // building the image allocates
+      if (!has_mx(w[j]))
+        return fail(ctx, LGH_ERR_INVALID_ARG,
+                    "the %zu x %zu matrix has no GEMM image; call lgh_q4_prepare_gemm before this call", w[j]->n,
+                    w[j]->k);
+    } else if (int r = ensure_mx(ctx, w[j])) {
+      return r;
+    }
+  }
+  // Tokens per launch: the activation image must fit 31-bit buffer offsets,
+  // and the chunk's scratch (image, row scales, split-K partials) must fit
+  // the fixed scratch when the call may not allocate.
   const size_t pp = (bpr + 1) / 2;
   const size_t rec_per_tile = pp * lgh::kMxARec;
   const size_t cap_tiles = lgh::kMxMaxBytes / rec_per_tile;
   if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", k);
-  const size_t chunk = std::min(m, (cap_tiles - 8) * 32);
   size_t rows = 0;
   for (int j = 0; j < nmat; j++) rows += w[j]->n;
-  const int splits = lgh::plan_q4_gemm_splits(w, nmat, chunk);
-  const size_t part_floats = splits > 1 ? static_cast<size_t>(splits) * chunk * rows : 0;
-  Carve cv;
-  const size_t o_mx = cv.take((chunk + 31) / 32 * rec_per_tile);
-  const size_t o_rs = cv.take(chunk * sizeof(float));
-  const size_t o_part = cv.take(part_floats * sizeof(float));
-  if (int r = ensure(ctx, &ctx->ws, &ctx->ws_bytes, cv.off)) return r;
-  char *ws = static_cast<char *>(ctx->ws);
+  struct Layout {
+    int splits;
+    size_t part_floats, o_mx, o_rs, o_part, bytes;
+  };
+  auto layout = [&](size_t c) {
+    Layout l{};
+    l.splits = lgh::plan_q4_gemm_splits(w, nmat, c);
+    l.part_floats = l.splits > 1 ? static_cast<size_t>(l.splits) * c * rows : 0;
+    Carve cv;
+    l.o_mx = cv.take((c + 31) / 32 * rec_per_tile);
+    l.o_rs = cv.take(c * sizeof(float));
+    l.o_part = cv.take(l.part_floats * sizeof(float));
+    l.bytes = cv.off;
+    return l;
+  };
+  size_t chunk = std::min(m, (cap_tiles - 8) * 32);
+  Layout lay = layout(chunk);
+  while (lay.bytes > wsp.limit() && chunk > 32) {  // halve, in whole 32-token tiles
+    chunk = std::max<size_t>(32, (chunk / 2 + 31) / 32 * 32);
+    lay = layout(chunk);
+  }
+  const size_t part_floats = lay.part_floats, o_mx = lay.o_mx, o_rs = lay.o_rs, o_part = lay.o_part;
+  char *ws = nullptr;
+  if (int r = wsp.get(lay.bytes, &ws)) return r;
   auto *mxa = reinterpret_cast<uint8_t *>(ws + o_mx);
   auto *rs = reinterpret_cast<float *>(ws + o_rs);
   auto *part = reinterpret_cast<float *>(ws + o_part);
@@ -568,9 +712,7 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (int r = check_mode(ctx, mode)) return r;
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
-  const lgh_q4 *ws[1] = {w};
-  float *ys[1] = {y_dev};
-  return gemm_multi_dev(ctx, ws, 1, x_dev, ys, m, mode);
+  return gemm_multi_dev(ctx, grow_ws(ctx), &w, 1, x_dev, &y_dev, m, mode);
 }
 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev, size_t tokens) {
@@ -788,7 +930,7 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
   if (norm_w_dev) LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, dim, tokens, eps, normed, ctx->stream));
   const lgh_q4 *gate_up[2] = {w1, w3};
   float *gu[2] = {g, u};
-  if (int r = gemm_multi_dev(ctx, gate_up, 2, normed, gu, tokens, LGH_ASSIGN)) return r;
+  if (int r = gemm_multi_dev(ctx, grow_ws(ctx), gate_up, 2, normed, gu, tokens, LGH_ASSIGN)) return r;
   LGH_HIP(ctx, lgh::launch_silu_mul(g, u, tokens * inter, ctx->stream));
   return lgh_q4_gemm_dev(ctx, w2, g, hidden_dev, tokens, LGH_ADD_F64);
 }
@@ -890,7 +1032,7 @@ int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, cons
     LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, k, tokens, eps, nd, ctx->stream));
     normed = nd;
   }
-  return gemm_multi_dev(ctx, w, nm, normed, y_dev, tokens, mode);
+  return gemm_multi_dev(ctx, grow_ws(ctx), w, nm, normed, y_dev, tokens, mode);
 }
 
 int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,
@@ -974,6 +1116,8 @@ int lgh_act_quant(lgh_ctx *ctx, const float *x, size_t m, size_t k, int8_t *qs, 
   return LGH_OK;
 }
 
+int lgh_gemv_plans_uncovered(void) { return lgh::gemv_plans_uncovered(); }
+
 int lgh_q4_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks, int32_t *out) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (nblocks == 0) return LGH_OK;
@@ -1024,7 +1168,7 @@ int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size
   if (m == 0 || w->n == 0 || w->bpr == 0) return LGH_OK;
   if (!qs || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
   if (int r = set_device(ctx)) return r;
-  if (!w->mx) return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu is too large for the GEMM path", w->n, w->k);
+  if (int r = ensure_mx(ctx, w)) return r;
   const size_t ob_bytes = m * w->n * w->bpr * 4;
   const size_t mx_bytes = (m + 31) / 32 * w->pp * lgh::kMxARec;
   if (mx_bytes >= lgh::kMxMaxBytes) return fail(ctx, LGH_ERR_SHAPE, "too many tokens for one hook call");

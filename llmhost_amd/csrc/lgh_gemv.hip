@@ -22,6 +22,14 @@
 
 namespace lgh {
 
+// Every (BPL, KW, W) shape plan_q4_gemv() can return, for both `narrow`
+// values; the Q4 and the Q8_0 dispatch tables are generated from this one
+// list, and lgh_gemv_plans_uncovered() checks the planner against it.
+#define LGH_GEMV_SHAPES(X)                                                                             \
+  X(1, 1, 16) X(1, 1, 8) X(1, 1, 4) X(2, 1, 16) X(2, 1, 8) X(2, 1, 4) X(3, 1, 16) X(3, 1, 8) X(3, 1, 4) \
+  X(4, 1, 16) X(4, 1, 8) X(4, 1, 4) X(1, 2, 4) X(2, 2, 4) X(4, 2, 16) X(2, 4, 16) X(2, 4, 8) X(2, 4, 4)  \
+  X(4, 4, 16) X(2, 8, 16) X(2, 8, 8) X(4, 8, 16) X(2, 16, 16) X(4, 16, 16)
+
 namespace {
 
 
@@ -228,6 +236,16 @@ template <int BPL, int KW, int W, bool PREQ = false, bool NORM = false>
 hipError_t launch_gemv16(const Q4GemvArgs &a, int total_wgs, hipStream_t st) {
   hipLaunchKernelGGL((q4_gemv_kernel<BPL, KW, W, PREQ, NORM>), dim3(total_wgs), dim3(W * kWave), 0, st, a);
   return hipGetLastError();
+}
+
+// The NORM prologue needs the whole row in one slice: it exists for KW = 1.
+template <int BPL, int KW, int W>
+hipError_t dispatch_q4(const Q4GemvArgs &a, int total_wgs, bool preq, bool norm, hipStream_t st) {
+  if (preq) return launch_gemv16<BPL, KW, W, true>(a, total_wgs, st);
+  if constexpr (KW == 1) {
+    if (norm) return launch_gemv16<BPL, KW, W, false, true>(a, total_wgs, st);
+  }
+  return launch_gemv16<BPL, KW, W, false>(a, total_wgs, st);
 }
 
 // ---- batched Q4 GEMV, 2 <= M <= 4 -----------------------------------------
@@ -808,6 +826,40 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
   return p;
 }
 
+bool gemv_shape_compiled(int bpl, int kw, int w) {
+#define LGH_HAS(BB, KK, WW) \
+  if (bpl == BB && kw == KK && w == WW) return true;
+  LGH_GEMV_SHAPES(LGH_HAS)
+#undef LGH_HAS
+  return false;
+}
+
+// plan_q4_gemv() over every row length it accepts (1..1024 blocks), 1..3
+// matrices, both `narrow` values, and total row counts on both sides of every
+// threshold the planner compares against (N = n * nmat against 192 * D for
+// D = 4W/KW, 3072, 4096, 8192, 16384, 32768) plus powers of two: the number
+// of plans whose shape has no compiled kernel.
+int gemv_plans_uncovered() {
+  static const long kBreaks[] = {192, 384, 768, 1536, 3072, 6144, 12288, 4096, 8192, 16384, 32768, 65536};
+  int missing = 0;
+  for (int narrow = 0; narrow < 2; narrow++)
+    for (int nmat = 1; nmat <= 3; nmat++)
+      for (size_t bpr = 1; bpr <= 1024; bpr++) {
+        auto check = [&](long n) {
+          if (n < 1) return;
+          const Q4GemvPlan p = plan_q4_gemv(static_cast<size_t>(n), bpr, nmat, narrow != 0);
+          if (p.ok && !gemv_shape_compiled(p.BPL, p.KW, p.W)) missing++;
+        };
+        for (long b : kBreaks)
+          for (long d = -2; d <= 2; d++) check((b + nmat - 1) / nmat + d);
+        for (long n = 1; n <= (1L << 20); n *= 2) {
+          check(n);
+          check(3 * n);
+        }
+      }
+  return missing;
+}
+
 // Quantize x once (act_quant_kernel) and run the codes GEMV instead when
 // the workgroups would re-quantize more than ~12M elements of x between them
 // (K=16384, N=8192: 19.5 -> 15.9 us; K=8192, N=16384 is even at 8.4M; a 4M
@@ -880,38 +932,10 @@ hipError_t launch_q4_gemv_multi(const lgh_q4 *const *w, float *const *y, int nma
   a.per_row = per_row;
   const int total = wgs[0] + wgs[1] + wgs[2];
   if (total == 0) return hipSuccess;
-#define LGH_G16(BB, KK, WW)                                                                          \
-  if (p.BPL == BB && p.KW == KK && p.W == WW)                                                        \
-  return preq ? launch_gemv16<BB, KK, WW, true>(a, total, st) : launch_gemv16<BB, KK, WW, false>(a, total, st)
-#define LGH_G16N(BB, KK, WW)                                                                         \
-  if (p.BPL == BB && p.KW == KK && p.W == WW)                                                        \
-  return preq   ? launch_gemv16<BB, KK, WW, true>(a, total, st)                                     \
-         : norm ? launch_gemv16<BB, KK, WW, false, true>(a, total, st)                              \
-                : launch_gemv16<BB, KK, WW, false>(a, total, st)
-  LGH_G16N(1, 1, 16);
-  LGH_G16N(1, 1, 8);
-  LGH_G16N(1, 1, 4);
-  LGH_G16N(2, 1, 16);
-  LGH_G16N(2, 1, 8);
-  LGH_G16N(2, 1, 4);
-  LGH_G16N(3, 1, 16);
-  LGH_G16N(3, 1, 8);
-  LGH_G16N(3, 1, 4);
-  LGH_G16N(4, 1, 16);
-  LGH_G16N(4, 1, 8);
-  LGH_G16N(4, 1, 4);
-  LGH_G16(2, 4, 16);
-  LGH_G16(2, 4, 8);
-  LGH_G16(2, 4, 4);
-  LGH_G16(2, 8, 16);
-  LGH_G16(2, 8, 8);
-  LGH_G16(2, 16, 16);
-  LGH_G16(4, 16, 16);
-  LGH_G16(4, 2, 16);
-  LGH_G16(4, 4, 16);
-  LGH_G16(4, 8, 16);
+#define LGH_G16(BB, KK, WW) \
+  if (p.BPL == BB && p.KW == KK && p.W == WW) return dispatch_q4<BB, KK, WW>(a, total, preq, norm, st);
+  LGH_GEMV_SHAPES(LGH_G16)
 #undef LGH_G16
-#undef LGH_G16N
   return hipErrorInvalidValue;
 }
 
@@ -1034,29 +1058,7 @@ hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t toke
       hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, false>), grid, dim3(WW * kWave), 0, st, a);      \
     return hipGetLastError();                                                                         \
   }
-  LGH_Q8(1, 1, 16);
-  LGH_Q8(1, 1, 8);
-  LGH_Q8(1, 1, 4);
-  LGH_Q8(2, 1, 16);
-  LGH_Q8(2, 1, 8);
-  LGH_Q8(2, 1, 4);
-  LGH_Q8(3, 1, 16);
-  LGH_Q8(3, 1, 8);
-  LGH_Q8(3, 1, 4);
-  LGH_Q8(4, 1, 16);
-  LGH_Q8(4, 1, 8);
-  LGH_Q8(4, 1, 4);
-  LGH_Q8(2, 4, 16);
-  LGH_Q8(2, 4, 8);
-  LGH_Q8(2, 4, 4);
-  LGH_Q8(2, 8, 16);
-  LGH_Q8(2, 8, 8);
-  LGH_Q8(2, 16, 16);
-  LGH_Q8(4, 16, 16);
-  LGH_Q8(4, 4, 16);
-  LGH_Q8(4, 8, 16);
-  LGH_Q8(1, 2, 4);
-  LGH_Q8(2, 2, 4);
+  LGH_GEMV_SHAPES(LGH_Q8)
 #undef LGH_Q8
   return hipErrorInvalidValue;
 }

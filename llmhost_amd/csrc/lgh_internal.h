@@ -34,6 +34,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "../../include/llm_gpu_hip.h"
@@ -61,8 +62,9 @@ struct lgh_q4 {
   size_t n = 0, k = 0, bpr = 0;
   uint8_t *qs = nullptr;   // n*bpr*16 bytes
   uint16_t *sc = nullptr;  // n*bpr halves (same allocation as qs)
-  uint8_t *mx = nullptr;   // GEMM operand image: nt*pp*kMxWRec bytes (own allocation)
-  size_t nt = 0, pp = 0;
+  uint8_t *mx = nullptr;   // GEMM operand image: nt*pp*kMxWRec bytes (own allocation), built on first GEMM use
+  size_t nt = 0, pp = 0;   // 32-row tiles, block pairs
+  std::mutex mx_mu;        // guards the one-time build of mx
 };
 
 struct lgh_q8 {
@@ -115,6 +117,9 @@ struct Q4GemvPlan {
 // narrow: prefer 8-wave workgroups once that gives >= 2 per CU (Q4 rows;
 // the Q8_0 head's 2x wider rows ran faster with 16 waves).
 Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow = true);
+// Plans (over a sweep of the planner's inputs) whose shape has no compiled
+// Q4 / Q8_0 GEMV kernel; 0 when the dispatch tables cover the planner.
+int gemv_plans_uncovered();
 bool q4_gemv_quantize_once(size_t n, size_t bpr, int nmat);
 hipError_t launch_q4_gemv(const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1, const float *x,
                           int mode, int per_row, hipStream_t stream);

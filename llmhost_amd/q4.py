@@ -13,7 +13,10 @@ with the computation done by libllm_gpu_hip.so on one MI355X:
 
 Operands are numpy arrays (host memory, synchronous, like the reference's
 slices) or torch tensors on the GPU (device memory, enqueued on the
-context's stream).  Where the reference `assert!`s (length mismatch,
+context's stream).  A call on torch tensors is ordered after the work already
+queued on torch's current stream, and torch's current stream is ordered after
+the call, so the kernels read what torch wrote before the call and torch reads
+what they wrote.  Where the reference `assert!`s (length mismatch,
 k % 32 != 0) these raise ``LghShapeError`` (a ValueError) and write nothing.
 
 A process-wide default context (device 0) plays the role of llm-cpu's
@@ -50,6 +53,8 @@ class Context:
             raise _ffi.LghError(code, lib().lgh_last_error(None).decode())
         self.handle = h
         self.device = device
+        self._stream_handle = lib().lgh_get_stream(h) or 0
+        self._torch_stream = None  # torch view of the context stream, made on first use
 
     def close(self) -> None:
         if getattr(self, "handle", None):
@@ -74,9 +79,34 @@ class Context:
     def set_stream(self, stream_handle: int | None) -> None:
         """Use a hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
         self.check(lib().lgh_set_stream(self.handle, C.c_void_p(stream_handle or 0)))
+        self._stream_handle = lib().lgh_get_stream(self.handle) or 0
+        self._torch_stream = None
 
     def stream(self) -> int:
-        return lib().lgh_get_stream(self.handle) or 0
+        return self._stream_handle
+
+    def trim(self) -> None:
+        """lgh_trim: release the context's workspaces (they grow again when needed)."""
+        self.check(lib().lgh_trim(self.handle))
+
+    def dev_call(self, launch) -> None:
+        """Run `launch` (which enqueues on the context stream) in torch's stream order: the context
+        stream first waits for torch's current stream, and torch's current stream then waits for
+        the context stream.  No waits when the two are the same stream."""
+        import torch
+
+        cur = torch.cuda.current_stream(self.device)
+        if cur.cuda_stream == self._stream_handle:
+            launch()
+            return
+        if self._torch_stream is None:
+            self._torch_stream = torch.cuda.ExternalStream(self._stream_handle, device=self.device)
+        ext = self._torch_stream
+        ext.wait_stream(cur)
+        try:
+            launch()
+        finally:
+            cur.wait_stream(ext)
 
     def sync(self) -> None:
         self.check(lib().lgh_sync(self.handle))
@@ -139,6 +169,15 @@ def _shape_assert(cond: bool, msg: str) -> None:
         raise LghShapeError(_ffi.LGH_ERR_SHAPE, msg)
 
 
+def _check_norm_w(norm_w, k: int) -> None:
+    """rms_norm asserts weight.len() == dim (crates/llm-cpu/src/ops.rs:9-11); the library reads k
+    floats of the norm weight, so a shorter one must never reach it."""
+    if norm_w is None:
+        return
+    size = norm_w.numel() if _is_torch(norm_w) else np.asarray(norm_w).size
+    _shape_assert(size == k, f"norm weight length {size} != {k}")
+
+
 # ---- matrices -----------------------------------------------------------------
 class Q4Matrix:
     """Device-resident Q4 matrix [n, k] (gemv_q4.rs:97-209)."""
@@ -158,7 +197,8 @@ class Q4Matrix:
         if _is_torch(blocks):
             _shape_assert(blocks.numel() * blocks.element_size() == n * (k // 32) * 18,
                           "blocks byte length != n*k/32*18")
-            ctx.check(lib().lgh_q4_upload_dev(ctx.handle, C.c_void_p(blocks.data_ptr()), n, k, C.byref(h)))
+            ctx.dev_call(lambda: ctx.check(
+                lib().lgh_q4_upload_dev(ctx.handle, C.c_void_p(blocks.data_ptr()), n, k, C.byref(h))))
         else:
             blocks = np.ascontiguousarray(blocks)
             _shape_assert(blocks.dtype == BLOCK_Q4 and blocks.size == n * (k // 32),
@@ -185,6 +225,14 @@ class Q4Matrix:
 
     def blocks_per_row(self) -> int:
         return self.k // BLOCK_SIZE
+
+    def prepare_gemm(self) -> None:
+        """lgh_q4_prepare_gemm: build the GEMM operand image now instead of on first GEMM use."""
+        self.ctx.check(lib().lgh_q4_prepare_gemm(self.ctx.handle, self._h))
+
+    def device_bytes(self) -> int:
+        """Device bytes held: nibble and scale planes, plus the GEMM image once built."""
+        return int(lib().lgh_q4_device_bytes(self._h))
 
     @property
     def handle(self) -> C.c_void_p:
@@ -297,9 +345,9 @@ class ActQ8:
         prev = ctx.act_quant()
         ctx.set_act_quant(mode)
         try:
-            ctx.check(lib().lgh_act_quant_dev(ctx.handle, _dev_ptr(x, "x"), m, k, _dev_ptr_of(qs, "qs", torch.int8),
-                                              _dev_ptr_of(sc, "scales", torch.float32),
-                                              _dev_ptr_of(su, "sums", torch.int32)))
+            ctx.dev_call(lambda: ctx.check(lib().lgh_act_quant_dev(
+                ctx.handle, _dev_ptr(x, "x"), m, k, _dev_ptr_of(qs, "qs", torch.int8),
+                _dev_ptr_of(sc, "scales", torch.float32), _dev_ptr_of(su, "sums", torch.int32))))
         finally:
             ctx.set_act_quant(prev)
         return cls(qs, sc, su)
@@ -321,7 +369,8 @@ def _gemm(w: Q4Matrix, x, out, m: int, mode: int) -> None:
     if _is_torch(x) or _is_torch(out):
         _shape_assert(x.numel() == m * w.k, f"x length {x.numel()} != {m}*{w.k}")
         _shape_assert(out.numel() == m * w.n, f"out length {out.numel()} != {m}*{w.n}")
-        ctx.check(lib().lgh_q4_gemm_dev(ctx.handle, w.handle, _dev_ptr(x, "x"), _dev_ptr(out, "out"), m, mode))
+        xp, op = _dev_ptr(x, "x"), _dev_ptr(out, "out")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_q4_gemm_dev(ctx.handle, w.handle, xp, op, m, mode)))
         return
     x = _host_f32(x, "x")
     out = _host_f32(out, "out")
@@ -348,9 +397,10 @@ def _gemv_prep(w: Q4Matrix, acts: ActQ8, out, mode: int) -> None:
         _shape_assert(acts.qs.numel() == w.k, f"acts length {acts.qs.numel()} != {w.k}")
         _shape_assert(acts.scales.numel() == w.k // 32, f"acts scales {acts.scales.numel()} != {w.k // 32}")
         _shape_assert(out.numel() == w.n, f"out length {out.numel()} != {w.n}")
-        ctx.check(lib().lgh_q4_gemv_prep_dev(ctx.handle, w.handle, _dev_ptr_of(acts.qs, "acts.qs", torch.int8),
-                                             _dev_ptr_of(acts.scales, "acts.scales", torch.float32),
-                                             _dev_ptr(out, "out"), mode))
+        qp = _dev_ptr_of(acts.qs, "acts.qs", torch.int8)
+        sp = _dev_ptr_of(acts.scales, "acts.scales", torch.float32)
+        op = _dev_ptr(out, "out")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_q4_gemv_prep_dev(ctx.handle, w.handle, qp, sp, op, mode)))
         return
     qs = np.ascontiguousarray(acts.qs, dtype=np.int8)
     sc = _host_f32(np.ascontiguousarray(acts.scales, dtype=np.float32), "acts.scales")
@@ -396,8 +446,9 @@ def gemv_q4_pair(w_gate: Q4Matrix, w_up: Q4Matrix, x, out_gate, out_up) -> None:
     if _is_torch(x):
         _shape_assert(x.numel() == w_gate.k, "x length != K")
         _shape_assert(out_gate.numel() == w_gate.n and out_up.numel() == w_up.n, "out length != N")
-        ctx.check(lib().lgh_q4_gemv_pair_dev(ctx.handle, w_gate.handle, w_up.handle, _dev_ptr(x, "x"),
-                                             _dev_ptr(out_gate, "out_gate"), _dev_ptr(out_up, "out_up")))
+        xp, gp, up = _dev_ptr(x, "x"), _dev_ptr(out_gate, "out_gate"), _dev_ptr(out_up, "out_up")
+        ctx.dev_call(lambda: ctx.check(
+            lib().lgh_q4_gemv_pair_dev(ctx.handle, w_gate.handle, w_up.handle, xp, gp, up)))
         return
     x = _host_f32(x, "x")
     out_gate = _host_f32(out_gate, "out_gate")
@@ -413,12 +464,14 @@ def rms_norm(x, weight, eps: float, out, ctx: Context | None = None) -> None:
     """rms_norm (crates/llm-cpu/src/ops.rs:8-23) over the rows of x (row length = weight size)."""
     ctx = ctx or default_context()
     if _is_torch(x):
-        _shape_assert(x.numel() % weight.numel() == 0 and out.numel() == x.numel(), "rms_norm shapes")
-        ctx.check(lib().lgh_rms_norm_dev(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(weight, "weight"), weight.numel(),
-                                         x.numel() // weight.numel(), float(eps), _dev_ptr(out, "out")))
+        _shape_assert(weight.numel() > 0 and x.numel() % weight.numel() == 0 and out.numel() == x.numel(),
+                      "rms_norm shapes")
+        xp, wp, op = _dev_ptr(x, "x"), _dev_ptr(weight, "weight"), _dev_ptr(out, "out")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_rms_norm_dev(ctx.handle, xp, wp, weight.numel(),
+                                                              x.numel() // weight.numel(), float(eps), op)))
         return
     x, weight, out = _host_f32(x, "x"), _host_f32(weight, "weight"), _host_f32(out, "out")
-    _shape_assert(x.size % weight.size == 0 and out.size == x.size, "rms_norm shapes")
+    _shape_assert(weight.size > 0 and x.size % weight.size == 0 and out.size == x.size, "rms_norm shapes")
     ctx.check(lib().lgh_rms_norm(ctx.handle, _np_ptr(x), _np_ptr(weight), weight.size, x.size // weight.size,
                                  float(eps), _np_ptr(out)))
 
@@ -428,7 +481,8 @@ def silu_mul(g, u, ctx: Context | None = None) -> None:
     ctx = ctx or default_context()
     if _is_torch(g):
         _shape_assert(g.numel() == u.numel(), "g/u lengths differ")
-        ctx.check(lib().lgh_silu_mul_dev(ctx.handle, _dev_ptr(g, "g"), _dev_ptr(u, "u"), g.numel()))
+        gp, up = _dev_ptr(g, "g"), _dev_ptr(u, "u")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_silu_mul_dev(ctx.handle, gp, up, g.numel())))
         return
     g, u = _host_f32(g, "g"), _host_f32(u, "u")
     _shape_assert(g.size == u.size, "g/u lengths differ")
@@ -442,11 +496,13 @@ def ffn_residual(w1: Q4Matrix, w3: Q4Matrix, w2: Q4Matrix, norm_w, eps: float, h
     torch)."""
     ctx = w1.ctx
     _shape_assert(w1.k == w3.k == w2.n and w1.n == w3.n == w2.k, "FFN shapes: W1, W3 [inter, dim], W2 [dim, inter]")
+    _check_norm_w(norm_w, w1.k)
     if _is_torch(hidden):
         _shape_assert(hidden.numel() == tokens * w1.k, "hidden length != tokens * dim")
         nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
-        ctx.check(lib().lgh_q4_ffn_residual_dev(ctx.handle, w1.handle, w3.handle, w2.handle, nw, float(eps),
-                                                _dev_ptr(hidden, "hidden"), tokens))
+        hp = _dev_ptr(hidden, "hidden")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_q4_ffn_residual_dev(ctx.handle, w1.handle, w3.handle, w2.handle,
+                                                                     nw, float(eps), hp, tokens)))
         return
     hidden = _host_f32(hidden, "hidden")
     _shape_assert(hidden.size == tokens * w1.k, "hidden length != tokens * dim")
@@ -466,14 +522,16 @@ def norm_gemv(ws, norm_w, eps: float, hidden, outs, tokens: int = 1, mode: int =
     ctx = ws[0].ctx
     k = ws[0].k
     _shape_assert(all(w.k == k for w in ws), "matrices must share K")
+    _check_norm_w(norm_w, k)
     handles = (C.c_void_p * len(ws))(*[w.handle.value for w in ws])
     if _is_torch(hidden):
         _shape_assert(hidden.numel() == tokens * k, "hidden length != tokens * K")
         _shape_assert(all(o.numel() == tokens * w.n for o, w in zip(outs, ws)), "out length != tokens * N")
         ptrs = (C.c_void_p * len(ws))(*[_dev_ptr(o, "out").value for o in outs])
         nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
-        ctx.check(lib().lgh_q4_norm_gemv_dev(ctx.handle, len(ws), handles, nw, float(eps), _dev_ptr(hidden, "hidden"),
-                                             ptrs, tokens, mode))
+        hp = _dev_ptr(hidden, "hidden")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_q4_norm_gemv_dev(ctx.handle, len(ws), handles, nw, float(eps), hp,
+                                                                  ptrs, tokens, mode)))
         return
     hidden = _host_f32(hidden, "hidden")
     outs = [_host_f32(o, "out") for o in outs]
@@ -489,6 +547,7 @@ def ffn_gate_up(w1: Q4Matrix, w3: Q4Matrix, norm_w, eps: float, hidden):
     """The gate/up stage of ffn_residual alone (test hook): returns g, u, h = silu(g) * u and
     h's PerBlock ActQ8 codes / scales as the down projection consumes them."""
     ctx = w1.ctx
+    _check_norm_w(norm_w, w1.k)
     hidden = _host_f32(hidden, "hidden")
     _shape_assert(hidden.size == w1.k, "hidden length != dim")
     n = w1.n
@@ -506,7 +565,8 @@ def q8_apply(m: Q8Matrix, x, tokens: int, out) -> None:
     ctx = m.ctx
     if _is_torch(x):
         _shape_assert(x.numel() == tokens * m.k and out.numel() == tokens * m.n, "length mismatch")
-        ctx.check(lib().lgh_q8_gemv_dev(ctx.handle, m.handle, _dev_ptr(x, "x"), _dev_ptr(out, "out"), tokens))
+        xp, op = _dev_ptr(x, "x"), _dev_ptr(out, "out")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_q8_gemv_dev(ctx.handle, m.handle, xp, op, tokens)))
         return
     x = _host_f32(x, "x")
     out = _host_f32(out, "out")
@@ -518,11 +578,13 @@ def q8_norm_apply(m: Q8Matrix, norm_w, eps: float, hidden, tokens: int, out) -> 
     """The final rms_norm then the Q8_0 head (crates/llm-engine/src/lfm2.rs:559-567): per token
     out = W rms_norm(hidden, norm_w, eps) (norm_w None: no norm), the norm in the GEMV's prologue."""
     ctx = m.ctx
+    _check_norm_w(norm_w, m.k)
     if _is_torch(hidden):
         _shape_assert(hidden.numel() == tokens * m.k and out.numel() == tokens * m.n, "length mismatch")
         nw = None if norm_w is None else _dev_ptr(norm_w, "norm_w")
-        ctx.check(lib().lgh_q8_norm_gemv_dev(ctx.handle, m.handle, nw, float(eps), _dev_ptr(hidden, "hidden"),
-                                             _dev_ptr(out, "out"), tokens))
+        hp, op = _dev_ptr(hidden, "hidden"), _dev_ptr(out, "out")
+        ctx.dev_call(lambda: ctx.check(lib().lgh_q8_norm_gemv_dev(ctx.handle, m.handle, nw, float(eps), hp, op,
+                                                                  tokens)))
         return
     hidden = _host_f32(hidden, "hidden")
     out = _host_f32(out, "out")

@@ -58,3 +58,9 @@ def test_init_reports_missing_device_or_wrong_arch():
     assert code in (_ffi.LGH_ERR_NO_DEVICE, _ffi.LGH_ERR_HIP, _ffi.LGH_ERR_ARCH)
     assert not h.value
     assert lib.lgh_last_error(None)
+
+
+def test_every_gemv_plan_has_a_compiled_kernel():
+    """The Q4 and Q8_0 GEMV planners only choose launch shapes the library compiled (a plan
+    without a kernel would fail at launch with LGH_ERR_HIP): host-only sweep in the library."""
+    assert _ffi.lib().lgh_gemv_plans_uncovered() == 0

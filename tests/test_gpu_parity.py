@@ -454,10 +454,12 @@ def test_gemm_add_and_per_row(gpu_ctx, oracle, per_row):
 # ---- Q8_0 GEMV ---------------------------------------------------------------------------
 @pytest.mark.parametrize("n,k,tokens", [(1536, 1536, 1), (77, 256, 3), (4096, 1536, 2), (65536, 1536, 1),
                                          (300, 4096, 2), (70, 8192, 1), (33, 16384, 1), (20, 32768, 2),
-                                         (5, 32, 3), (1, 64, 1), (130, 96, 4)])
+                                         (5, 32, 3), (1, 64, 1), (130, 96, 4), (16384, 4096, 1),
+                                         (16400, 2080, 2)])
 def test_q8_gemv_matches_oracle(gpu_ctx, oracle, n, k, tokens):
-    """Every plan of the Q8_0 GEMV: one K slice (1..4 blocks per lane), 4 / 8 / 16 slices,
-    rows not a multiple of 4, several tokens (grid.y), the N=65536 head."""
+    """Every plan of the Q8_0 GEMV: one K slice (1..4 blocks per lane), 2 / 4 / 8 / 16 slices
+    (2 slices of 4 blocks per lane: rows of 65-128 blocks at N >= 16384, a tied head of hidden
+    2080-4096), rows not a multiple of 4, several tokens (grid.y), the N=65536 head."""
     blocks = synth.q8_blocks(n + k, n, k)
     x = synth.activations(tokens + k, tokens, k)
     w = q4.Q8Matrix.from_blocks(n, k, blocks, gpu_ctx)
