@@ -46,3 +46,41 @@ def gpu_ctx():
     from llmhost_amd import q4
 
     return q4.default_context()
+
+
+def code_flip_bound(blocks, n, k, q_ref, s_ref, q_got, s_got):
+    """Upper bound, per output row, on |W (q_got * s_got) - W (q_ref * s_ref)| in exact arithmetic
+    for a Q4 matrix W (BlockQ4 [n, k/32]) applied to two ActQ8 quantizations of (nearly) the same
+    vector: q codes [k], s block scales [k/32].  Per block kb with dots D = sum w q:
+        |s' D' - s D| <= |s' - s| sum |w| |q'| + s sum |w| |q' - q|,
+    times the block's weight scale.  Zero when the codes and scales agree; each flipped code adds
+    |nibble| * sw * sa.  Also returns the number of codes and of block scales that differ."""
+    from llmhost_amd import formats
+
+    bpr = k // 32
+    nib = np.abs(formats.q4_nibbles(blocks.reshape(n, bpr)).astype(np.int64))  # [n, bpr, 32]
+    sw = blocks.reshape(n, bpr)["scale"].view(np.float16).astype(np.float64)    # [n, bpr]
+    q_ref = np.asarray(q_ref, np.int64).reshape(bpr, 32)
+    q_got = np.asarray(q_got, np.int64).reshape(bpr, 32)
+    s_ref = np.asarray(s_ref, np.float64).reshape(bpr)
+    s_got = np.asarray(s_got, np.float64).reshape(bpr)
+    a = np.einsum("ibj,bj->ib", nib, np.abs(q_got))             # sum |w| |q'| per row and block
+    b = np.einsum("ibj,bj->ib", nib, np.abs(q_got - q_ref))     # sum |w| |q' - q|
+    bound = (sw * (np.abs(s_got - s_ref)[None, :] * a + s_ref[None, :] * b)).sum(axis=1)
+    flips = int(np.count_nonzero(q_got != q_ref))
+    scale_diffs = int(np.count_nonzero(s_got != s_ref))
+    return bound, flips, scale_diffs
+
+
+def assert_close_with_flips(got, ref, bound, what=""):
+    """The gate tolerance plus a per-element allowance (e.g. code_flip_bound's)."""
+    got = np.asarray(got, dtype=np.float64).ravel()
+    ref = np.asarray(ref, dtype=np.float64).ravel()
+    bound = np.asarray(bound, dtype=np.float64).ravel()
+    err = np.abs(got - ref)
+    lim = ATOL + RTOL * np.abs(ref) + bound * (1 + 1e-6)
+    bad = err > lim
+    if bad.any():
+        i = np.flatnonzero(bad)[0]
+        raise AssertionError(f"{what}: {bad.sum()} / {bad.size} out of tolerance; first at {i}: got {got[i]!r} "
+                             f"ref {ref[i]!r} allowance {bound[i]:.3e}")

@@ -1,0 +1,79 @@
+"""Parity at the exact shapes the benchmark times, against the oracle's production (VNNI-512)
+kernel, plus the steady state of the two-buffer (5-wave) GEMM pipeline.
+
+Shapes: the ragged batched GEMMs (M = 4 / 16 / 64, K = 2048, N = 8192), the four prefill GEMMs
+(M = 512 / 2048 x K = 2048, N = 10752 and K = 10752, N = 2048), the decode GEMVs of the headline
+step and of the 16-layer sweep, and the Q8_0 GEMV.  Inputs are the benchmark's generators.
+"""
+
+import numpy as np
+import pytest
+
+from llmhost_amd import q4, synth
+
+from .conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm_vs_oracle(ctx, oracle, m, n, k, seed, scalar=False):
+    print(f"[shape] m={m} n={n} k={k}", flush=True)
+    blocks = synth.q4_blocks(seed, n, k)
+    x = synth.activations(seed + 1, m, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, ctx)
+    got = np.zeros((m, n), dtype=np.float32)
+    q4.gemm_q4(w, x, got, m)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    assert_close(got, oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_VNNI, threads=8), what="vs vnni")
+    if scalar:
+        assert_close(got, oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_SCALAR, threads=8), what="vs scalar")
+    w.free()
+    return got
+
+
+@pytest.mark.parametrize("m", [4, 16, 64])
+def test_ragged_gemm_benchmark_shape(gpu_ctx, oracle, m):
+    """Ragged batches: M rows packed from sequences of 1-8 tokens (rows are independent, so the
+    packing only sets M), K = 2048, N = 8192."""
+    _gemm_vs_oracle(gpu_ctx, oracle, m, 8192, 2048, 300 + m, scalar=True)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 10752, 2048), (512, 2048, 10752), (2048, 10752, 2048),
+                                   (2048, 2048, 10752)])
+def test_prefill_gemm_benchmark_shape(gpu_ctx, oracle, m, n, k):
+    """M = 512 (three-buffer form; split-K at K = 10752) and M = 2048 (the two-buffer 5-wave form
+    at K = 2048: 5376 workgroups, 32 block pairs)."""
+    _gemm_vs_oracle(gpu_ctx, oracle, m, n, k, 400 + m + k)
+
+
+@pytest.mark.parametrize("k", [256, 288])
+def test_five_wave_gemm_steady_state(gpu_ctx, oracle, k):
+    """The two-buffer pipeline refills a buffer after computing it: 4 and 5 block pairs (an even
+    and an odd count) over 5376 workgroups (M = 2048, N = 10752) run its steady state, against
+    the oracle's scalar (reference-order) kernel."""
+    _gemm_vs_oracle(gpu_ctx, oracle, 2048, 10752, k, 500 + k, scalar=True)
+
+
+@pytest.mark.parametrize("n,k", [(1536, 1536), (8192, 1536), (1536, 8192), (2048, 1536)])
+def test_decode_gemv_benchmark_shape(gpu_ctx, oracle, n, k):
+    """The headline step's up / down GEMVs, the sweep's q/k/v (2048 x 1536) and o (1536 x 1536)."""
+    blocks = synth.q4_blocks(600 + n + k, n, k)
+    x = synth.normal_f32(601 + k, k)
+    w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = np.zeros(n, dtype=np.float32)
+    q4.gemv_q4(w, x, got)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    assert_close(got, oracle.gemv_q4(mat, x, kernel=oracle.KERNEL_SCALAR, threads=8), what="vs scalar")
+    assert_close(got, oracle.gemv_q4(mat, x, kernel=oracle.KERNEL_VNNI, threads=8), what="vs vnni")
+    w.free()
+
+
+def test_q8_gemv_benchmark_shape(gpu_ctx, oracle):
+    n = k = 1536
+    blocks = synth.q8_blocks(71, n, k)
+    x = synth.normal_f32(72, k)
+    w = q4.Q8Matrix.from_blocks(n, k, blocks, gpu_ctx)
+    got = np.zeros(n, dtype=np.float32)
+    q4.q8_apply(w, x, 1, got)
+    assert_close(got, oracle.q8_apply(blocks, n, k, x, 1, threads=8), what="q8")
+    w.free()
