@@ -117,7 +117,7 @@ int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks);
  * 18 B/32 nibble and scale planes; the first call that routes the matrix to
  * the GEMM (m >= 65, long rows at m >= 49, or k > 32768) builds the image
  * itself, which allocates -- so call this before capturing such a call in a
- * graph.  LGH_ERR_SHAPE if
+ * graph or passing the matrix to lgh_q4_gemm_dev_noalloc.  LGH_ERR_SHAPE if
  * the image would exceed 2 GiB.  No reference counterpart: llm-cpu's Q4Matrix
  * packs its tiles (and AMX panels) at load, gemv_q4.rs:116-209. */
 int lgh_q4_prepare_gemm(lgh_ctx *ctx, const lgh_q4 *w);
@@ -175,6 +175,23 @@ int lgh_act_quant_dev(lgh_ctx *ctx, const float *x_dev, size_t m, size_t k, int8
 int lgh_q4_gemm(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, size_t m, int mode);
 int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m,
                     int mode);
+
+/* The same product as lgh_q4_gemm_dev, for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  No counterpart in the reference (llm-cpu allocates
+ * its activation buffers per call, gemv_q4.rs:725-798).  Every scratch buffer
+ * of the call (activation images and codes, split-K partials) comes from one
+ * fixed device array of LGH_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends; the call allocates, frees and synchronizes nothing.  Token
+ * chunks shrink until their scratch fits; a call whose 32-token chunk still
+ * needs more returns LGH_ERR_SHAPE.  Routes that need the matrix's GEMM image
+ * return LGH_ERR_INVALID_ARG unless lgh_q4_prepare_gemm has built it.  Every
+ * context on a GPU shares that GPU's array and it keeps the last call's
+ * contents: calls that overlap on one GPU (several contexts or streams)
+ * race, so the caller serializes them.  Results equal lgh_q4_gemm_dev's. */
+#define LGH_NOALLOC_SCRATCH_BYTES (32u << 20)
+int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m,
+                            int mode);
 
 /* ---- Q8_0 GEMV ------------------------------------------------------------
  * q8_apply (crates/llm-engine/src/weights.rs:194-227), reached through

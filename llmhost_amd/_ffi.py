@@ -65,6 +65,7 @@ SIGNATURES = {
     "lgh_q4_gemv_pair_dev": (_I, [_P, _P, _P, _P, _P, _P]),
     "lgh_q4_gemm": (_I, [_P, _P, _P, _P, _SZ, _I]),
     "lgh_q4_gemm_dev": (_I, [_P, _P, _P, _P, _SZ, _I]),
+    "lgh_q4_gemm_dev_noalloc": (_I, [_P, _P, _P, _P, _SZ, _I]),
     "lgh_q8_gemv": (_I, [_P, _P, _P, _P, _SZ]),
     "lgh_q8_gemv_dev": (_I, [_P, _P, _P, _P, _SZ]),
     "lgh_act_quant": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),

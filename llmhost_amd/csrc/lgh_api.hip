@@ -16,10 +16,21 @@
 
 #include "lgh_internal.h"
 
+// Fixed device scratch of lgh_q4_gemm_dev_noalloc: one copy per GPU, held
+// until the process ends.  Host code never uses this name as an address (on
+// the host it is a stand-in, not device memory): lgh_init looks up each
+// device's copy with hipGetSymbolAddress and every call passes that pointer.
+__device__ __align__(256) uint8_t scratch[LGH_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_init_err;
 
+// Device address of `scratch` per device, looked up once per device with
+// that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices] = {};
 
 int fail(lgh_ctx *ctx, int code, const char *fmt, ...) {
   char buf[512];
@@ -54,14 +65,15 @@ int set_device(lgh_ctx *ctx) {
 
 // Grow-only device buffer; waits for queued work before releasing the old one.
 // A stream under graph capture cannot synchronize or allocate: growing there
-// fails with LGH_ERR_CAPTURE (the caller warms the shape up eagerly first).
+// fails with LGH_ERR_CAPTURE (the caller warms the shape up eagerly first, or
+// uses lgh_q4_gemm_dev_noalloc).
 int ensure(lgh_ctx *ctx, void **buf, size_t *cap, size_t bytes) {
   if (bytes <= *cap) return LGH_OK;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
     return fail(ctx, LGH_ERR_CAPTURE,
                 "a workspace must grow to %zu bytes while the stream is being captured; run the same "
-                "shape once before capturing",
+                "shape once before capturing, or call lgh_q4_gemm_dev_noalloc",
                 bytes);
   if (*buf) {
     LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -277,6 +289,21 @@ int lgh_init(int device, lgh_ctx **out) {
     return fail(nullptr, LGH_ERR_HIP, "stream creation failed: %s", hipGetErrorString(e));
   }
   ctx->stream = ctx->own_stream;
+  if (device < kMaxDevices) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[device]) {
+      void *p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return fail(nullptr, LGH_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", device,
+                    hipGetErrorString(e));
+      }
+      g_scratch[device] = p;
+    }
+    ctx->scratch = g_scratch[device];
+  }
   *out = ctx;
   return LGH_OK;
 }
@@ -713,6 +740,21 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   return gemm_multi_dev(ctx, grow_ws(ctx), &w, 1, x_dev, &y_dev, m, mode);
+}
+
+// lgh_q4_gemm_dev with every scratch buffer taken from the device's fixed
+// scratch array instead of the context workspace: no allocation, no free, no
+// synchronisation.  Token chunks shrink until their scratch fits; a call that
+// needs more than the array holds even for 32 tokens fails with LGH_ERR_SHAPE.
+int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mode(ctx, mode)) return r;
+  if (m == 0 || w->n == 0) return LGH_OK;
+  if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
+  if (!ctx->scratch) return fail(ctx, LGH_ERR_INVALID_ARG, "device %d has no fixed scratch", ctx->device);
+  const Ws fixed{ctx, static_cast<char *>(ctx->scratch), LGH_NOALLOC_SCRATCH_BYTES};
+  return gemm_multi_dev(ctx, fixed, &w, 1, x_dev, &y_dev, m, mode);
 }
 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev, size_t tokens) {

@@ -55,6 +55,9 @@ struct lgh_ctx {
   // FFN block intermediates (h's codes / scales, or h in f32).
   void *ffn = nullptr;
   size_t ffn_bytes = 0;
+  // This device's fixed scratch array (LGH_NOALLOC_SCRATCH_BYTES), shared by
+  // every context on the device; looked up once per device at lgh_init.
+  void *scratch = nullptr;
 };
 
 struct lgh_q4 {
