@@ -98,6 +98,18 @@ int lgh_sync(lgh_ctx *ctx);
  * counterpart (llm-cpu keeps no device buffers). */
 int lgh_trim(lgh_ctx *ctx);
 
+/* ---- device buffers ---------------------------------------------------------
+ * Backend::alloc (crates/llm-core/src/backend.rs:4-13; the CPU backend's
+ * Vec<f32>, crates/llm-cpu/src/lib.rs:65-75): a device buffer of `len` f32
+ * elements, zero-filled, for the *_dev entry points.  len == 0 gives NULL.
+ * lgh_buffer_write / lgh_buffer_read copy host <-> device (synchronous) --
+ * the copy methods backend.rs:3 leaves to the first real backend.  Free with
+ * lgh_buffer_free (waits for the context stream first). */
+int lgh_buffer_alloc(lgh_ctx *ctx, size_t len, float **out);
+void lgh_buffer_free(lgh_ctx *ctx, float *buf);
+int lgh_buffer_write(lgh_ctx *ctx, float *dst_dev, const float *src, size_t len);
+int lgh_buffer_read(lgh_ctx *ctx, float *dst, const float *src_dev, size_t len);
+
 /* ---- weights ------------------------------------------------------------
  * Q4Matrix::from_blocks (crates/llm-cpu/src/gemv_q4.rs:128-149): upload
  * row-major BlockQ4[n][k/32] from host memory and repack on the device.
@@ -124,6 +136,25 @@ int lgh_q4_prepare_gemm(lgh_ctx *ctx, const lgh_q4 *w);
 /* Device bytes the matrix holds: the nibble and scale planes, plus the GEMM
  * image once built. */
 size_t lgh_q4_device_bytes(const lgh_q4 *w);
+
+/* ---- device images (pre-packed load format) ------------------------------------
+ * The matrix exactly as it sits in HBM, so that a load is one copy with no
+ * repack kernel: the Q4 image is the nibble plane (n*k/32 x 16 B, the
+ * repaired nibble order), the f16 scale plane (n*k/32 x 2 B) and, with_gemm,
+ * the GEMM operand image; the Q8_0 image is the code plane (n*k/32 x 32 B)
+ * and the scale plane.  Export writes `bytes` (= *_image_bytes) to host
+ * memory, building the GEMM image first if asked for; import allocates a
+ * matrix from such an image (bytes must match n, k).  The image format is
+ * this library's own (a file container around it: llmhost_amd/packfile.py);
+ * it stands in for the pre-packed .lfmb container llm-quant plans
+ * (ARCHITECTURE.md:101) and for Q4Matrix::from_blocks' per-load repack
+ * (crates/llm-cpu/src/gemv_q4.rs:128-149). */
+size_t lgh_q4_image_bytes(const lgh_q4 *w, int with_gemm);
+int lgh_q4_export(lgh_ctx *ctx, const lgh_q4 *w, int with_gemm, void *dst, size_t bytes);
+int lgh_q4_import(lgh_ctx *ctx, const void *src, size_t bytes, size_t n, size_t k, int with_gemm, lgh_q4 **out);
+size_t lgh_q8_image_bytes(const lgh_q8 *w);
+int lgh_q8_export(lgh_ctx *ctx, const lgh_q8 *w, void *dst, size_t bytes);
+int lgh_q8_import(lgh_ctx *ctx, const void *src, size_t bytes, size_t n, size_t k, lgh_q8 **out);
 void lgh_q4_free(lgh_q4 *w);
 size_t lgh_q4_rows(const lgh_q4 *w);
 size_t lgh_q4_cols(const lgh_q4 *w);
@@ -156,8 +187,8 @@ int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *w_gate, const lgh_q4 *w_up,
  * GEMV on activations already quantized by ActQ8 -- codes int8[k] and block
  * scales f32[k/32] as lgh_act_quant(_dev) writes them, in either act-quant
  * mode (the sums are not read).  The reference's Q4Kernel argument has no
- * counterpart (one device kernel).  K <= 32768.  Device codes 16-byte and
- * scales 4-byte aligned. */
+ * counterpart (one device kernel; K > 32768 runs the GEMM on the same codes).
+ * Device codes 16-byte and scales 4-byte aligned. */
 int lgh_q4_gemv_prep(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, const float *scales, float *y, int mode);
 int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, const float *scales_dev,
                          float *y_dev, int mode);
@@ -196,7 +227,9 @@ int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, f
 /* ---- Q8_0 GEMV ------------------------------------------------------------
  * q8_apply (crates/llm-engine/src/weights.rs:194-227), reached through
  * OutputHead::apply (weights.rs:186-192): per token, y[n] = W[n,k] @ x[k]
- * with per-block ActQ8 activations.  Assign mode only, as in the reference. */
+ * with per-block ActQ8 activations.  Assign mode only, as in the reference.
+ * Any K and any number of tokens (rows past 32768 elements are summed in
+ * K ranges of 32768, added in f32). */
 int lgh_q8_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *x, float *y, size_t tokens);
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev,
                     size_t tokens);

@@ -44,12 +44,22 @@ SIGNATURES = {
     "lgh_get_stream": (_P, [_P]),
     "lgh_sync": (_I, [_P]),
     "lgh_trim": (_I, [_P]),
+    "lgh_buffer_alloc": (_I, [_P, _SZ, C.POINTER(_P)]),
+    "lgh_buffer_free": (None, [_P, _P]),
+    "lgh_buffer_write": (_I, [_P, _P, _P, _SZ]),
+    "lgh_buffer_read": (_I, [_P, _P, _P, _SZ]),
     "lgh_q4_upload": (_I, [_P, _P, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_upload_dev": (_I, [_P, _P, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_from_f32": (_I, [_P, _P, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_download": (_I, [_P, _P, _P]),
     "lgh_q4_prepare_gemm": (_I, [_P, _P]),
     "lgh_q4_device_bytes": (_SZ, [_P]),
+    "lgh_q4_image_bytes": (_SZ, [_P, _I]),
+    "lgh_q4_export": (_I, [_P, _P, _I, _P, _SZ]),
+    "lgh_q4_import": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, C.POINTER(_P)]),
+    "lgh_q8_image_bytes": (_SZ, [_P]),
+    "lgh_q8_export": (_I, [_P, _P, _P, _SZ]),
+    "lgh_q8_import": (_I, [_P, _P, _SZ, _SZ, _SZ, C.POINTER(_P)]),
     "lgh_q4_free": (None, [_P]),
     "lgh_q4_rows": (_SZ, [_P]),
     "lgh_q4_cols": (_SZ, [_P]),

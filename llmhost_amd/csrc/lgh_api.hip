@@ -359,6 +359,56 @@ int lgh_trim(lgh_ctx *ctx) {
   return LGH_OK;
 }
 
+// ---- device buffers -----------------------------------------------------------
+int lgh_buffer_alloc(lgh_ctx *ctx, size_t len, float **out) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!out) return fail(ctx, LGH_ERR_INVALID_ARG, "null buffer out-pointer");
+  *out = nullptr;
+  if (len == 0) return LGH_OK;
+  if (len > SIZE_MAX / sizeof(float)) return fail(ctx, LGH_ERR_SHAPE, "buffer of %zu floats is too large", len);
+  if (int r = set_device(ctx)) return r;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, len * sizeof(float));
+  if (e != hipSuccess)
+    return fail(ctx, LGH_ERR_OOM, "hipMalloc(%zu bytes) for a buffer failed: %s", len * sizeof(float),
+                hipGetErrorString(e));
+  e = hipMemsetAsync(p, 0, len * sizeof(float), ctx->stream);  // zeroed, as CpuBackend::alloc
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(ctx, e, "buffer clear");
+  }
+  *out = static_cast<float *>(p);
+  return LGH_OK;
+}
+
+void lgh_buffer_free(lgh_ctx *ctx, float *buf) {
+  if (!ctx || !buf) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);  // queued work may still use it
+  (void)hipFree(buf);
+}
+
+int lgh_buffer_write(lgh_ctx *ctx, float *dst_dev, const float *src, size_t len) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (len == 0) return LGH_OK;
+  if (!dst_dev || !src) return fail(ctx, LGH_ERR_INVALID_ARG, "null buffer");
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(dst_dev, src, len * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_buffer_read(lgh_ctx *ctx, float *dst, const float *src_dev, size_t len) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (len == 0) return LGH_OK;
+  if (!dst || !src_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null buffer");
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(dst, src_dev, len * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
 // ---- weights -------------------------------------------------------------
 namespace {
 // Wait for the repack of a fresh matrix (the GEMM image is built on first use).
@@ -424,6 +474,113 @@ int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks) {
   LGH_HIP(ctx, lgh::launch_q4_unpack(w->qs, w->sc, nb, static_cast<uint8_t *>(ctx->stage), ctx->stream));
   LGH_HIP(ctx, hipMemcpyAsync(blocks, ctx->stage, bytes, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+// ---- device images: the matrix as it sits in HBM, for a load that is one copy ----
+size_t lgh_q4_image_bytes(const lgh_q4 *w, int with_gemm) {
+  if (!w) return 0;
+  const size_t nb = w->n * w->bpr;
+  return nb * 18 + (with_gemm ? w->nt * w->pp * lgh::kMxWRec : 0);
+}
+
+int lgh_q4_export(lgh_ctx *ctx, const lgh_q4 *w, int with_gemm, void *dst, size_t bytes) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (bytes != lgh_q4_image_bytes(w, with_gemm))
+    return fail(ctx, LGH_ERR_SHAPE, "image of %zu x %zu needs %zu bytes, got %zu", w->n, w->k,
+                lgh_q4_image_bytes(w, with_gemm), bytes);
+  if (bytes == 0) return LGH_OK;
+  if (!dst) return fail(ctx, LGH_ERR_INVALID_ARG, "null destination");
+  if (int r = set_device(ctx)) return r;
+  const size_t nb = w->n * w->bpr;
+  char *d = static_cast<char *>(dst);
+  if (with_gemm)
+    if (int r = ensure_mx(ctx, w)) return r;
+  LGH_HIP(ctx, hipMemcpyAsync(d, w->qs, nb * 16, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(d + nb * 16, w->sc, nb * 2, hipMemcpyDeviceToHost, ctx->stream));
+  if (with_gemm)
+    LGH_HIP(ctx, hipMemcpyAsync(d + nb * 18, w->mx, w->nt * w->pp * lgh::kMxWRec, hipMemcpyDeviceToHost,
+                                ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q4_import(lgh_ctx *ctx, const void *src, size_t bytes, size_t n, size_t k, int with_gemm, lgh_q4 **out) {
+  if (int r = check_shape(ctx, src, n, k, out)) return r;
+  *out = nullptr;
+  if (int r = set_device(ctx)) return r;
+  lgh_q4 *w = nullptr;
+  if (int r = alloc_matrix(ctx, n, k, 16, &w)) return r;
+  if (with_gemm && !mx_fits(w) && n * w->bpr) {
+    free_matrix(w);
+    return fail(ctx, LGH_ERR_SHAPE, "%zu x %zu has no GEMM image (too large for the GEMM path)", n, k);
+  }
+  const size_t need = lgh_q4_image_bytes(w, with_gemm), nb = n * w->bpr;
+  if (bytes != need) {
+    free_matrix(w);
+    return fail(ctx, LGH_ERR_SHAPE, "image of %zu x %zu needs %zu bytes, got %zu", n, k, need, bytes);
+  }
+  const char *s = static_cast<const char *>(src);
+  hipError_t e = hipSuccess;
+  if (nb) e = hipMemcpyAsync(w->qs, s, nb * 16, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess && nb) e = hipMemcpyAsync(w->sc, s + nb * 16, nb * 2, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess && with_gemm && nb) {
+    void *p = nullptr;
+    const size_t mb = w->nt * w->pp * lgh::kMxWRec;
+    e = hipMalloc(&p, mb);
+    if (e == hipSuccess) {
+      w->mx = static_cast<uint8_t *>(p);
+      e = hipMemcpyAsync(w->mx, s + nb * 18, mb, hipMemcpyHostToDevice, ctx->stream);
+    }
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_matrix(w);
+    return hip_fail(ctx, e, "Q4 image import");
+  }
+  *out = w;
+  return LGH_OK;
+}
+
+size_t lgh_q8_image_bytes(const lgh_q8 *w) { return w ? w->n * w->bpr * LGH_BLOCK_Q8_BYTES : 0; }
+
+int lgh_q8_export(lgh_ctx *ctx, const lgh_q8 *w, void *dst, size_t bytes) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (bytes != lgh_q8_image_bytes(w))
+    return fail(ctx, LGH_ERR_SHAPE, "image needs %zu bytes, got %zu", lgh_q8_image_bytes(w), bytes);
+  if (bytes == 0) return LGH_OK;
+  if (!dst) return fail(ctx, LGH_ERR_INVALID_ARG, "null destination");
+  if (int r = set_device(ctx)) return r;
+  const size_t nb = w->n * w->bpr;
+  char *d = static_cast<char *>(dst);
+  LGH_HIP(ctx, hipMemcpyAsync(d, w->qs, nb * 32, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipMemcpyAsync(d + nb * 32, w->sc, nb * 2, hipMemcpyDeviceToHost, ctx->stream));
+  LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return LGH_OK;
+}
+
+int lgh_q8_import(lgh_ctx *ctx, const void *src, size_t bytes, size_t n, size_t k, lgh_q8 **out) {
+  if (int r = check_shape(ctx, src, n, k, out)) return r;
+  *out = nullptr;
+  const size_t nb = n * (k / 32);
+  if (bytes != nb * LGH_BLOCK_Q8_BYTES)
+    return fail(ctx, LGH_ERR_SHAPE, "image of %zu x %zu needs %zu bytes, got %zu", n, k, nb * LGH_BLOCK_Q8_BYTES,
+                bytes);
+  if (int r = set_device(ctx)) return r;
+  lgh_q8 *w = nullptr;
+  if (int r = alloc_matrix(ctx, n, k, 32, &w)) return r;
+  const char *s = static_cast<const char *>(src);
+  hipError_t e = hipSuccess;
+  if (nb) e = hipMemcpyAsync(w->qs, s, nb * 32, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess && nb) e = hipMemcpyAsync(w->sc, s + nb * 32, nb * 2, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_matrix(w);
+    return hip_fail(ctx, e, "Q8 image import");
+  }
+  *out = w;
   return LGH_OK;
 }
 
@@ -570,9 +727,25 @@ int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, co
   if (!y_dev || (w->k && (!qs_dev || !scales_dev))) return fail(ctx, LGH_ERR_INVALID_ARG, "null codes/scales/y");
   if (!aligned16(qs_dev) || (reinterpret_cast<uintptr_t>(scales_dev) & 3u))
     return fail(ctx, LGH_ERR_INVALID_ARG, "codes must be 16-byte and scales 4-byte aligned");
-  if (!lgh::plan_q4_gemv(w->n, w->bpr, 1).ok)
-    return fail(ctx, LGH_ERR_SHAPE, "K=%zu: the prepared-activation GEMV supports K <= 32768", w->k);
   if (int r = set_device(ctx)) return r;
+  if (!lgh::plan_q4_gemv(w->n, w->bpr, 1).ok) {
+    // K > 32768: the codes and scales become the GEMM's activation image (one token), and the
+    // GEMM folds every block as the GEMV does.
+    if (int r = ensure_mx(ctx, w)) return r;
+    const lgh_q4 *ws1[1] = {w};
+    const int splits = lgh::plan_q4_gemm_splits(ws1, 1, 1);
+    const size_t part_floats = splits > 1 ? static_cast<size_t>(splits) * w->n : 0;
+    Carve cv;
+    const size_t o_mx = cv.take(w->pp * lgh::kMxARec), o_part = cv.take(part_floats * sizeof(float));
+    char *ws = nullptr;
+    if (int r = grow_ws(ctx).get(cv.off, &ws)) return r;
+    auto *mxa = reinterpret_cast<uint8_t *>(ws + o_mx);
+    LGH_HIP(ctx, lgh::launch_act_split_mx(qs_dev, scales_dev, 1, w->k, mxa, ctx->stream));
+    float *ys[1] = {y_dev};
+    LGH_HIP(ctx, lgh::launch_q4_gemm(ws1, 1, mxa, ys, 1, mode, reinterpret_cast<float *>(ws + o_part), part_floats,
+                                     ctx->stream));
+    return LGH_OK;
+  }
   LGH_HIP(ctx, lgh::launch_q4_gemv_codes(w, qs_dev, scales_dev, y_dev, mode, ctx->stream));
   return LGH_OK;
 }
@@ -763,8 +936,6 @@ int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_
   if (tokens == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
-  if (w->k > lgh::kQ8GemvMaxK) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", lgh::kQ8GemvMaxK);
-  if (tokens > 65535) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports at most 65535 tokens per call");
   if (int r = set_device(ctx)) return r;
   LGH_HIP(ctx, lgh::launch_q8_gemv(w, x_dev, y_dev, tokens, nullptr, 0.0f, ctx->stream));
   return LGH_OK;
@@ -778,10 +949,16 @@ int lgh_q8_norm_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w_dev,
   if (!y_dev || (w->k && !hidden_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/y");
   if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
     return fail(ctx, LGH_ERR_INVALID_ARG, "hidden and norm weight must be 16-byte aligned");
-  if (w->k > lgh::kQ8GemvMaxK) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports K <= %zu", lgh::kQ8GemvMaxK);
-  if (tokens > 65535) return fail(ctx, LGH_ERR_SHAPE, "Q8_0 GEMV supports at most 65535 tokens per call");
   if (int r = set_device(ctx)) return r;
-  LGH_HIP(ctx, lgh::launch_q8_gemv(w, hidden_dev, y_dev, tokens, w->k ? norm_w_dev : nullptr, eps, ctx->stream));
+  const float *x = hidden_dev, *nw = w->k ? norm_w_dev : nullptr;
+  if (nw && w->k > lgh::kQ8GemvMaxK) {  // rows longer than the prologue covers: rms_norm first
+    if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, tokens * w->k * sizeof(float))) return r;
+    float *nd = static_cast<float *>(ctx->ffn);
+    LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, nw, w->k, tokens, eps, nd, ctx->stream));
+    x = nd;
+    nw = nullptr;
+  }
+  LGH_HIP(ctx, lgh::launch_q8_gemv(w, x, y_dev, tokens, nw, eps, ctx->stream));
   return LGH_OK;
 }
 
@@ -1220,7 +1397,7 @@ int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size
   char *st = static_cast<char *>(ctx->stage);
   auto *mxa = reinterpret_cast<uint8_t *>(st + omx);
   LGH_HIP(ctx, hipMemcpyAsync(st + oq, qs, m * w->k, hipMemcpyHostToDevice, ctx->stream));
-  LGH_HIP(ctx, lgh::launch_act_split_mx(reinterpret_cast<int8_t *>(st + oq), m, w->k, mxa, ctx->stream));
+  LGH_HIP(ctx, lgh::launch_act_split_mx(reinterpret_cast<int8_t *>(st + oq), nullptr, m, w->k, mxa, ctx->stream));
   LGH_HIP(ctx, lgh::launch_q4_mfma_block_dots(w, mxa, m, reinterpret_cast<int32_t *>(st + oo), ctx->stream));
   LGH_HIP(ctx, hipMemcpyAsync(out, st + oo, ob_bytes, hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));

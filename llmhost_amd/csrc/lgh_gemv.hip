@@ -15,6 +15,7 @@
 //   * 4 DPP adds give every lane of a DPP row its row's slice sum; slice sums
 //     meet in LDS and are added in slice order (deterministic), then Assign
 //     or AddF64 (gemv_q4.rs:486-497) after removing the x16 (exact).
+#include <algorithm>
 #include <type_traits>
 
 #include "lgh_device.h"
@@ -653,15 +654,19 @@ hipError_t launch_mma(const Q4MmaArgs &a, hipStream_t st) {
 
 // ---- Q8_0 GEMV (crates/llm-engine/src/weights.rs:194-227) ---------------
 struct Q8GemvArgs {
-  const int8_t *qs;    // [n][bpr][32], natural order
-  const uint16_t *sc;  // f16 scales [n][bpr]
-  const float *x;      // [tokens][k]
+  const int8_t *qs;    // [n][stride][32], natural order
+  const uint16_t *sc;  // f16 scales [n][stride]
+  const float *x;      // [tokens][xstride], this launch's K range starting at x
   float *y;            // [tokens][n]
   const float *nw;     // NORM: rms_norm weight [k]
   double inv_k;        // NORM: 1 / k in f64 (ops.rs:12)
   float eps;
   int n;
-  int bpr;
+  int bpr;      // blocks of the K range this launch covers
+  int stride;   // blocks per row of the matrix
+  int kb_off;   // first block of the range
+  int xstride;  // floats per token row of x
+  int add;      // 0: y = partial; 1: y += partial in f32 (K ranges after the first)
 };
 
 // The Q4 GEMV's mapping (one weight row per 16-lane DPP row, W waves =
@@ -699,7 +704,7 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   const size_t tok = blockIdx.y;
 
   // (1) x, then (1b) the x-before-weights barrier for long rows.
-  const auto xr = make_rsrc(a.x + tok * static_cast<size_t>(bpr) * 32, static_cast<uint32_t>(bpr) * 128u);
+  const auto xr = make_rsrc(a.x + tok * static_cast<size_t>(a.xstride), static_cast<uint32_t>(bpr) * 128u);
   const auto nr = make_rsrc(a.nw, NORM ? static_cast<uint32_t>(bpr) * 128u : 0u);
   float4 xv[XJ];
   float4 nv[NORM ? XJ : 1];
@@ -726,15 +731,17 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   }
 
   // (2) every weight load of this lane (rows past n fall outside the resource).
-  const size_t blk0 = static_cast<size_t>(row0) * bpr;
-  const auto wr = make_rsrc(a.qs + blk0 * 32, static_cast<uint32_t>(rows * bpr) * 32u);
-  const auto sr = make_rsrc(a.sc + blk0, static_cast<uint32_t>(rows * bpr) * 2u);
+  const int stride = a.stride;
+  const size_t blk0 = static_cast<size_t>(row0) * stride + a.kb_off;
+  const uint32_t span = rows > 0 ? static_cast<uint32_t>((rows - 1) * stride + bpr) : 0u;
+  const auto wr = make_rsrc(a.qs + blk0 * 32, span * 32u);
+  const auto sr = make_rsrc(a.sc + blk0, span * 2u);
   uint4 w0[BPL], w1[BPL];
   uint16_t s[BPL];
 #pragma unroll
   for (int j = 0; j < BPL; j++) {
     const int kb = kb0 + 16 * j;
-    const uint32_t blk = static_cast<uint32_t>(r * bpr + kb);
+    const uint32_t blk = static_cast<uint32_t>(r * stride + kb);
     w0[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u : kOOB);
     w1[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u : kOOB);
     s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
@@ -767,7 +774,7 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   acc += dpp<0x140>(acc);
   float *y = a.y + tok * static_cast<size_t>(a.n);
   if constexpr (KW == 1) {
-    if (c == 0 && r < rows) y[row0 + r] = acc;
+    if (c == 0 && r < rows) y[row0 + r] = a.add ? y[row0 + r] + acc : acc;
   } else {
     if (c == 0) s_part[(rg * 4 + r) * KW + ks] = acc;
     __syncthreads();
@@ -775,7 +782,7 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
       float sum = 0.0f;
 #pragma unroll
       for (int k = 0; k < KW; k++) sum += s_part[(rg * 4 + lane) * KW + k];
-      y[row0 + lane] = sum;
+      y[row0 + lane] = a.add ? y[row0 + lane] + sum : sum;
     }
   }
 }
@@ -1040,14 +1047,39 @@ hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float
   return hipErrorInvalidValue;
 }
 
-// The Q8_0 GEMV takes the Q4 GEMV's plan (same row mapping, same limits).
+hipError_t launch_q8_range(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
+                           size_t b0, size_t nb, bool add, hipStream_t st);
+
+// The Q8_0 GEMV takes the Q4 GEMV's plan (same row mapping).  Rows longer than
+// one launch covers (K > 32768) run as consecutive K ranges of <= 32768,
+// each adding its partial sums onto y in f32, and tokens beyond the grid's
+// 65535 run as further launches.  The norm prologue needs whole rows: norm_w
+// is only accepted with K <= 32768 (the API norms longer rows first).
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
                           hipStream_t st) {
   if (w->n == 0 || tokens == 0) return hipSuccess;
-  const Q4GemvPlan p = plan_q4_gemv(w->n, w->bpr, 1, false);
-  if (!p.ok || tokens > 65535) return hipErrorInvalidValue;  // rejected by the API before launch
+  constexpr size_t kMaxBpr = kQ8GemvMaxK / 32, kMaxTok = 65535;
+  if (norm_w && w->bpr > kMaxBpr) return hipErrorInvalidValue;  // the API norms first
+  for (size_t t0 = 0; t0 < tokens; t0 += kMaxTok) {
+    const size_t nt = std::min(kMaxTok, tokens - t0);
+    for (size_t b0 = 0; b0 < w->bpr; b0 += kMaxBpr) {
+      const size_t nb = std::min(kMaxBpr, w->bpr - b0);
+      hipError_t e = launch_q8_range(w, x + t0 * w->k + b0 * 32, y + t0 * w->n, nt, norm_w, eps, b0, nb,
+                                     b0 > 0, st);
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
+}
+
+// One launch of the Q8_0 GEMV over blocks [b0, b0 + nb) of every row.
+hipError_t launch_q8_range(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
+                           size_t b0, size_t nb, bool add, hipStream_t st) {
+  const Q4GemvPlan p = plan_q4_gemv(w->n, nb, 1, false);
+  if (!p.ok || tokens > 65535) return hipErrorInvalidValue;
   Q8GemvArgs a{w->qs, w->sc, x, y, norm_w, 1.0 / static_cast<double>(w->k), eps, static_cast<int>(w->n),
-               static_cast<int>(w->bpr)};
+               static_cast<int>(nb), static_cast<int>(w->bpr), static_cast<int>(b0), static_cast<int>(w->k),
+               add ? 1 : 0};
   const dim3 grid(static_cast<unsigned>(p.wgs_per_mat), static_cast<unsigned>(tokens));
   const bool norm = norm_w != nullptr;
 #define LGH_Q8(BB, KK, WW)                                                                            \

@@ -93,8 +93,10 @@ hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t stream);
 // mode; row_scale is scratch for m floats) straight into mt*pp records.
 hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, uint8_t *mxa,
                                float *row_scale, hipStream_t stream);
-// Same record layout from already-quantized int8 activations (scales left 0).
-hipError_t launch_act_split_mx(const int8_t *aq, size_t m, size_t k, uint8_t *mxa, hipStream_t stream);
+// Same record layout from already-quantized int8 activations aq [m][k] and
+// their block scales [m][k/32] (scales null: 0).
+hipError_t launch_act_split_mx(const int8_t *aq, const float *scales, size_t m, size_t k, uint8_t *mxa,
+                               hipStream_t stream);
 
 hipError_t launch_q4_repack(const uint8_t *raw_blocks, size_t nblocks, uint8_t *qs, uint16_t *sc,
                             hipStream_t stream);
@@ -187,8 +189,9 @@ hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row,
                                 float *row_scale, hipStream_t stream);
 hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
                               int mode, hipStream_t stream);
-// Q8_0 GEMV for k <= kQ8GemvMaxK (the Q4 GEMV plan's reach); with norm_w not
-// null each token's row is rms_norm'd in the prologue (eps as rms_norm).
+// Q8_0 GEMV; K ranges of kQ8GemvMaxK (the Q4 GEMV plan's reach) and 65535
+// tokens per launch.  With norm_w not null (k <= kQ8GemvMaxK only) each
+// token's row is rms_norm'd in the prologue (eps as rms_norm).
 constexpr size_t kQ8GemvMaxK = 32768;
 hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
                           hipStream_t stream);

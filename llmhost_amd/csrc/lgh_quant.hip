@@ -316,7 +316,8 @@ __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__r
   }
 }
 
-__global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__restrict__ aq, int m, int bpr,
+__global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__restrict__ aq,
+                                                                const float *__restrict__ as, int m, int bpr,
                                                                 int pp, size_t groups, uint8_t *mxa) {
   const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
   if (gi >= groups) return;
@@ -328,7 +329,10 @@ __global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__
   codes24_hl(q, vh, vl);
   uint8_t *rec = mxa + (static_cast<size_t>(t >> 5) * pp + (b >> 1)) * kMxARec;
   store_hl_group8(rec, b & 1, t & 31, vh, vl);
-  if (g == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = 0.0f;
+  if (g == 0) {
+    const float sa = (as && t < m && b < bpr) ? as[static_cast<size_t>(t) * bpr + b] : 0.0f;
+    reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (t & 31)] = sa;
+  }
 }
 
 // Activations for the matrix-core batch GEMV, in its MFMA register layouts
@@ -407,12 +411,13 @@ hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row,
   return hipGetLastError();
 }
 
-hipError_t launch_act_split_mx(const int8_t *aq, size_t m, size_t k, uint8_t *mxa, hipStream_t st) {
+hipError_t launch_act_split_mx(const int8_t *aq, const float *scales, size_t m, size_t k, uint8_t *mxa,
+                               hipStream_t st) {
   const size_t bpr = k / 32, pp = (bpr + 1) / 2, mt = (m + 31) / 32;
   if (m == 0 || bpr == 0) return hipSuccess;
   const size_t groups = mt * 32 * pp * 2;
   hipLaunchKernelGGL(act_split_mx_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, aq,
-                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), groups, mxa);
+                     scales, static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), groups, mxa);
   return hipGetLastError();
 }
 

@@ -84,3 +84,26 @@ def assert_close_with_flips(got, ref, bound, what=""):
         i = np.flatnonzero(bad)[0]
         raise AssertionError(f"{what}: {bad.sum()} / {bad.size} out of tolerance; first at {i}: got {got[i]!r} "
                              f"ref {ref[i]!r} allowance {bound[i]:.3e}")
+
+
+def q8_exact_terms(blocks, n, k, qs, sa):
+    """q8_apply's value in exact arithmetic for BlockQ8_0 [n, k/32] on ActQ8 codes qs [t, k] and
+    block scales sa [t, k/32]: every term f32(dot) * sw * sa is exact in f64 (a 15-bit integer
+    dot, an 11-bit f16 scale and a 24-bit f32 scale), and so is their sum up to f64 rounding.
+    Returns (y [t, n], R [t, n]) with R = sqrt(sum of squared terms), the scale of the partial
+    sums an f32 accumulation walks through."""
+    nb = k // 32
+    w = blocks.reshape(n, nb)["qs"].astype(np.int64)                       # [n, nb, 32]
+    sw = blocks.reshape(n, nb)["scale"].view(np.float16).astype(np.float64)  # [n, nb]
+    q = np.asarray(qs, np.int64).reshape(-1, nb, 32)
+    s = np.asarray(sa, np.float64).reshape(-1, nb)
+    dots = np.einsum("nbj,tbj->tnb", w, q)
+    terms = dots.astype(np.float64) * sw[None] * s[:, None, :]
+    return terms.sum(axis=-1), np.sqrt((terms * terms).sum(axis=-1))
+
+
+def summation_allowance(R, nterms):
+    """What the order of an f32 summation of nterms terms can move the result by, at the scale R of
+    its partial sums: 8 u sqrt(n) R with u = 2^-24 (the probabilistic rounding-error bound's form;
+    8 standard deviations)."""
+    return 8.0 * 2.0 ** -24 * np.sqrt(nterms) * np.asarray(R, np.float64)
