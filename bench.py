@@ -78,8 +78,9 @@ class GpuBench:
         del raw
         return blocks, mats
 
-    def timed(self, fn, iters, warmup):
-        """ms per iteration of fn(i), i = 0..iters-1, replayed from a HIP graph.
+    def timed(self, fn, iters, warmup, reps=1):
+        """ms per iteration of fn(i), i = 0..iters-1, replayed from a HIP graph (a list of `reps`
+        such figures, one per replay, when reps > 1).
 
         The warm-up runs eagerly (it also sizes every workspace, so nothing is
         allocated under capture); the timed region is one replay of a graph
@@ -96,16 +97,19 @@ class GpuBench:
             for i in range(iters):
                 fn(i)
         # replay() launches on torch's current stream: make it the library's.
+        samples = []
         with torch.cuda.stream(self.stream):
             graph.replay()  # first replay uploads the graph
             torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(self.stream)
-            graph.replay()
-            e1.record(self.stream)
-        torch.cuda.synchronize()
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(self.stream)
+                graph.replay()
+                e1.record(self.stream)
+                torch.cuda.synchronize()
+                samples.append(e0.elapsed_time(e1) / iters)
         del graph
-        return e0.elapsed_time(e1) / iters  # ms per iteration
+        return samples if reps > 1 else samples[0]  # ms per iteration
 
 
 def gemv_workload(gb: GpuBench, steps: int, warmup: int):
@@ -180,7 +184,9 @@ def gemm_case(gb: GpuBench, m, n, k, iters, seed):
     torch, q4 = gb.torch, gb.q4
     from llmhost_amd import synth
 
-    _, mats = gb.copies(n, k, seed, 2 * MALL_BYTES if m <= 64 else 1)
+    _, mats = gb.copies(n, k, seed, 2 * MALL_BYTES + (64 << 20))
+    for w in mats:  # GEMM images up front: none may be built while the timed graph is captured
+        w.prepare_gemm()
     x = torch.from_numpy(synth.activations(seed + 1, m, k)).cuda()
     y = torch.zeros(m, n, device="cuda")
     C = len(mats)
@@ -318,6 +324,10 @@ def block_input_case(gb: GpuBench, iters, rows, dim=1536, tokens=1):
             for j, n in enumerate(rows)]
     sets = [[q4.Q4Matrix.from_blocks(n, dim, raws[j], gb.ctx) for j, n in enumerate(rows)] for _ in range(count)]
     del raws
+    if tokens > 64:  # the GEMM route: build every copy's GEMM image before the timed graph is captured
+        for ws in sets:
+            for w in ws:
+                w.prepare_gemm()
     hidden = torch.from_numpy(synth.normal_f32(710, tokens * dim)).cuda()
     nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(711, dim)).astype(np.float32)).cuda()
     normed = torch.zeros(tokens * dim, device="cuda")
@@ -379,7 +389,8 @@ def decode_step_case(gb: GpuBench, iters, layers=16, dim=1536, inter=8192, vocab
             q4.ffn_residual(m["w1"], m["w3"], m["w2"], nw, 1e-5, hidden)
         q4.q8_norm_apply(head, nw, 1e-5, hidden, 1, logits)
 
-    ms = gb.timed(step, iters, 2)
+    samples = gb.timed(step, iters, 2, reps=5)
+    ms = float(np.median(samples))
     layer_bytes = sum(w.n * (w.k // 32) * 18 for w in L[0].values())
     total = layers * layer_bytes + vocab * (dim // 32) * 34
     for m in L:
@@ -388,17 +399,91 @@ def decode_step_case(gb: GpuBench, iters, layers=16, dim=1536, inter=8192, vocab
     head.free()
     return {"layers": layers, "us": ms * 1e3, "weight_bytes": total, "gbs": total / (ms * 1e-3) / 1e9,
             "frac_hbm": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "launches": 4 * layers + 2,
-            "tokens_per_s": 1e3 / ms}
+            "tokens_per_s": 1e3 / ms, "samples_ms": [round(v, 5) for v in samples]}
 
 
-def cpu_baseline(target_s: float = 12.0):
-    """The oracle's llm-cpu restatement (runtime-dispatched kernel, pinned
-    pool) on this host, over rotating packed copies larger than the LLC."""
+def cpu_available() -> int:
+    """CPUs this process may run on: its affinity mask, bounded by a cgroup CPU quota when one is
+    set (a GPU box's share of a larger host)."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _sys_jiffies():
+    """(busy, total) jiffies of the whole machine from /proc/stat (bench/src/main.rs:103-117)."""
+    with open("/proc/stat") as f:
+        v = [int(t) for t in f.readline().split()[1:]]
+    total = sum(v)
+    return total - v[3] - (v[4] if len(v) > 4 else 0), total
+
+
+def _own_jiffies():
+    """utime + stime of this process (bench/src/main.rs:120-126)."""
+    with open("/proc/self/stat") as f:
+        rest = f.read().rsplit(")", 1)[1].split()
+    return int(rest[11]) + int(rest[12])
+
+
+def _loadavg():
+    try:
+        with open("/proc/loadavg") as f:
+            return float(f.read().split()[0])
+    except (OSError, ValueError):
+        return float("nan")
+
+
+def cpu_timed(fn, target_s: float):
+    """Call fn() until target_s has passed; returns (calls, seconds, noise) with the reference's noise
+    record (bench/src/main.rs:238-251): CPUs kept busy by other processes during the run."""
+    load0, (b0, t0j), o0 = _loadavg(), _sys_jiffies(), _own_jiffies()
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        fn(calls)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    load1, (b1, t1j), o1 = _loadavg(), _sys_jiffies(), _own_jiffies()
+    ncpu = len(os.sched_getaffinity(0))
+    other = max(0.0, (b1 - b0) - (o1 - o0)) / max(1, t1j - t0j) * ncpu
+    return calls, el, {"load_before": load0, "load_after": load1, "other_cpus": round(other, 3),
+                       "noisy": other > 1.0}
+
+
+def cpu_baseline(target_s: float = 10.0, row_s: float = 4.0):
+    """The oracle's llm-cpu restatement (runtime-dispatched kernel: VNNI-512 > AVX2 > scalar,
+    pinned pool of pool.rs) on this host, on 1 thread and on every available core (capped at
+    pool.rs's 64), over rotating packed copies larger than the LLC: the headline GEMV step (the
+    returned row), and rows for the M=512 prefill GEMM and the 16-layer decode sweep."""
     import oracle
     from llmhost_amd import synth
 
-    threads = min(16, len(os.sched_getaffinity(0)), oracle.lib().oq_max_threads())
+    cores = min(cpu_available(), oracle.lib().oq_max_threads())
     kern = oracle.detect_kernel()
+    host = {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "available": cpu_available(), "kernel": oracle.kernel_name(kern)}
+    rows = []
+
+    # headline: up 1536 -> 8192 + down 8192 -> 1536 per step
     shapes = [(8192, 1536), (1536, 8192)]
     ncopies = 24  # 24 x 2 x 7.9 MB of packed CPU tiles, beyond a typical LLC
     mats, xs = [], []
@@ -407,25 +492,70 @@ def cpu_baseline(target_s: float = 12.0):
         mats.append([oracle.Q4Matrix(n, k, blocks) for _ in range(ncopies)])
         xs.append(synth.normal_f32(201 + i, k))
     outs = [np.zeros(n, dtype=np.float32) for n, _ in shapes]
-    for j in range(2):  # warm-up / page-in
-        for s in range(2):
-            oracle.gemv_q4(mats[s][j], xs[s], outs[s], threads=threads)
     step_bytes = sum(q4_bytes(n, k) for n, k in shapes)
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        for s in range(2):
-            oracle.gemv_q4(mats[s][steps % ncopies], xs[s], outs[s], threads=threads)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= target_s:
-            break
-    gbs = steps * step_bytes / el / 1e9
-    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+    headline = None
+    for threads in (1, cores):
+        def step(i, threads=threads):
+            for s in range(2):
+                oracle.gemv_q4(mats[s][i % ncopies], xs[s], outs[s], threads=threads)
+        step(0)
+        step(1)  # warm-up / page-in
+        calls, el, noise = cpu_timed(step, target_s if threads == cores else row_s)
+        gbs = calls * step_bytes / el / 1e9
+        row = {"workload": "Q4 GEMV up K=1536,N=8192 + down K=8192,N=1536", "threads": threads,
+               "value": round(gbs, 3), "unit": "GB/s", "frac_hbm_of_gpu": round(gbs / HBM_PEAK_GBS, 5),
+               "ms_per_step": round(el / calls * 1e3, 4), "steps": calls, "seconds": round(el, 2), **noise}
+        rows.append(row)
+        if threads == cores:
+            headline = (gbs, calls, el)
+    del mats
+
+    # prefill GEMM M=512, K=2048, N=10752 (4 rotating copies of 13.8 MB of tiles)
+    m, n, k = 512, 10752, 2048
+    blocks = synth.q4_blocks(912, n, k)
+    gm = [oracle.Q4Matrix(n, k, blocks) for _ in range(4)]
+    x = synth.activations(913, m, k)
+    out = np.zeros((m, n), dtype=np.float32)
+    for threads in (1, cores):
+        oracle.gemm_q4(gm[0], x, m, out=out, threads=threads)
+        calls, el, noise = cpu_timed(lambda i, t=threads: oracle.gemm_q4(gm[i % 4], x, m, out=out, threads=t), row_s)
+        tops = calls * 2.0 * m * n * k / el / 1e12
+        rows.append({"workload": f"Q4 GEMM M={m} K={k} N={n}", "threads": threads, "value": round(tops, 4),
+                     "unit": "TOPS", "ms_per_call": round(el / calls * 1e3, 3), "calls": calls,
+                     "seconds": round(el, 2), **noise})
+    del gm
+
+    # 16-layer decode sweep (qkv 1536->2048, o, gate/up pair 1536->8192, down 8192->1536 AddF64)
+    H, F, L = 1536, 8192, 16
+    layer_shapes = [("qkv", 2048, H), ("o", H, H), ("gate", F, H), ("up", F, H), ("down", H, F)]
+    layers = [{name: oracle.Q4Matrix(n, kk, synth.q4_blocks(500 + j, n, kk))
+               for j, (name, n, kk) in enumerate(layer_shapes)} for _ in range(L)]
+    xh = synth.normal_f32(7, H)
+    qkv, h = np.zeros(2048, np.float32), np.zeros(H, np.float32)
+
+    def sweep(_i, threads):
+        for lw in layers:
+            oracle.gemv_q4(lw["qkv"], xh, qkv, threads=threads)
+            oracle.gemv_q4(lw["o"], xh, h, threads=threads)
+            g, u = oracle.gemv_q4_pair(lw["gate"], lw["up"], xh, threads=threads)
+            oracle.gemv_q4(lw["down"], g, h, add=True, threads=threads)
+
+    sweep_bytes = L * (q4_bytes(2048, H) + q4_bytes(H, H) + 2 * q4_bytes(F, H) + q4_bytes(H, F))
+    for threads in (1, cores):
+        sweep(0, threads)
+        calls, el, noise = cpu_timed(lambda i, t=threads: sweep(i, t), row_s)
+        rows.append({"workload": "Q4 decode sweep, 16 layers (391.6 MB)", "threads": threads,
+                     "value": round(calls * sweep_bytes / el / 1e9, 3), "unit": "GB/s",
+                     "tokens_per_s": round(calls / el, 3), "ms_per_step": round(el / calls * 1e3, 3),
+                     "steps": calls, "seconds": round(el, 2), **noise})
+    del layers
+
+    gbs, calls, el = headline
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "kernel": oracle.kernel_name(kern),
-            "sample": f"{steps} steps (up 1536->8192 + down 8192->1536 Q4 GEMV, fp32 x in, act-quant "
-                      f"included) over {ncopies} rotating packed copies, {el:.1f} s wall",
-            "ms_per_step": el / steps * 1e3}
+            "sample": f"{calls} steps (up 1536->8192 + down 8192->1536 Q4 GEMV, fp32 x in, act-quant "
+                      f"included) on {cores} pinned threads over {ncopies} rotating packed copies, {el:.1f} s",
+            "ms_per_step": round(el / calls * 1e3, 4), "host": host, "rows": rows}
 
 
 def counters_mode(iters: int = 50) -> None:
@@ -504,6 +634,48 @@ def rocprof_avg_us(name: str):
     return None
 
 
+def _stats(xs):
+    xs = sorted(xs)
+    mean = sum(xs) / len(xs)
+    sd = math.sqrt(sum((v - mean) ** 2 for v in xs) / max(1, len(xs) - 1)) if len(xs) > 1 else 0.0
+    return {"tok_s_mean": mean, "tok_s_stdev": sd, "tok_s_p50": xs[len(xs) // 2], "tok_s_min": xs[0],
+            "tok_s_max": xs[-1]}
+
+
+def _git(*args):
+    import subprocess
+
+    try:
+        return subprocess.run(["git", *args], cwd=ROOT, capture_output=True, text=True, timeout=10).stdout.strip()
+    except (OSError, subprocess.SubprocessError):
+        return ""
+
+
+def jsonl_rows(extra, cpu):
+    """Decode rows in the reference benchmark's JSONL schema (bench/src/main.rs:255-266): test "tg1"
+    is one decode token through the 16-layer matmul stack (the engine's mixing steps are not on
+    this path), tokens/s per sample."""
+    common = {"commit": _git("rev-parse", "--short", "HEAD"), "dirty": bool(_git("status", "--porcelain")),
+              "cpu": cpu_model(), "unix_time": int(time.time())}
+    rows = []
+    step = extra.get("decode_step_16L_chained")
+    if step:
+        xs = [1e3 / v for v in step["samples_ms"]]
+        rows.append({"engine": "llm-gpu-hip", "model": "LFM2-700M-shaped 16-layer matmul stack (synthetic)",
+                     "weights": "Q4_32 + Q8_0 head", "test": "tg1", "threads": None, "device": "MI355X",
+                     "runs": len(xs), **_stats(xs), "samples": xs, "load_before": None, "load_after": None,
+                     "other_cpus": None, "noisy": False, **common})
+    for r in (cpu or {}).get("rows", []):
+        if "tokens_per_s" not in r:
+            continue
+        xs = [r["tokens_per_s"]]
+        rows.append({"engine": "llm-cpu (oracle restatement)", "model": "16-layer Q4 decode sweep (synthetic)",
+                     "weights": "Q4_32", "test": "tg1", "threads": r["threads"], "runs": 1, **_stats(xs),
+                     "samples": xs, "load_before": r["load_before"], "load_after": r["load_after"],
+                     "other_cpus": r["other_cpus"], "noisy": r["noisy"], **common})
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -513,6 +685,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline GEMV only")
     ap.add_argument("--counters", action="store_true",
                     help="eager launches for rocprofv3 --pmc runs (no JSON line)")
+    ap.add_argument("--jsonl", default=None,
+                    help="also append decode rows in the reference benchmark's JSONL schema to this file")
     args = ap.parse_args()
     if args.counters:
         counters_mode()
@@ -540,6 +714,8 @@ def main():
             extra[f"prefill_gemm_m{m}_k{k}_n{n}"] = gemm_case(gb, m, n, k, 10, 400 + m + k)
         log("[bench] q8 gemv")
         extra["q8_gemv_k1536_n1536"] = q8_case(gb, 200)
+        log("[bench] Q4 GEMV K=N=1536 (the target's smallest shape)")
+        extra["q4_gemv_k1536_n1536"] = q4_head_case(gb, 200, 1536, 1536)
         log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
         extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
         extra["final_norm_q8_head_k1536_n65536"] = q8_head_norm_case(gb, 20)
@@ -592,6 +768,10 @@ def main():
                             "roofline": {"bound": "mfma", "achieved": round(g["tops"], 2),
                                          "peak": INT8_PEAK_TOPS, "unit": "TOPS (int8 dense)",
                                          "frac": round(g["frac_int8"], 4)}}
+    if args.jsonl:
+        with open(args.jsonl, "a") as f:
+            for row in jsonl_rows(extra, cpu):
+                f.write(json.dumps(row) + "\n")
     print(json.dumps(out), flush=True)
 
 
