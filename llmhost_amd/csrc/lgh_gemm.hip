@@ -40,6 +40,7 @@ constexpr long kSplitTarget = 512;  // two workgroups per CU (M=512, K=10752, N=
 constexpr size_t kSplitMinPairs = 64;  // K >= 4096
 constexpr size_t kSplitPairs = 16;     // K >= 1024 per split
 constexpr long kFiveWaveWgs = 5120;  // four rounds of 5 workgroups on each of 256 CUs
+constexpr size_t kWideTokens = 2048;  // 128 x 64 workgroup tiles from this many tokens (no split K)
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]
@@ -194,6 +195,45 @@ __device__ __forceinline__ StageOffs stage_offsets(int wn, int wm) {
 template <class C, int TN, int TM>
 __device__ __forceinline__ void compute_stage(const char *buf, const StageOffs &o, float (&acc)[TN][TM][16]) {
   const v32f zero32 = {};
+  if constexpr (TN * TM > 1) {
+    // Several tiles per wave: all operands first (LDS reads), then per tile
+    // its scales' outer product, its two block dots and its folds, so one
+    // tile's products are live at a time (same per-element arithmetic and
+    // block order as below).
+    float xs[TN], ys[TM];
+    v8i A[2][TN], B[2][TM];
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) xs[tn] = *reinterpret_cast<const float *>(buf + o.ws + tn * kWRec);
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) ys[tm] = *reinterpret_cast<const float *>(buf + o.as + tm * kARec);
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) A[b][tn] = mx_operand(buf + o.a16[b] + tn * kWRec, buf + o.a8[b] + tn * kWRec);
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++) B[b][tm] = mx_operand(buf + o.b16[b] + tm * kARec, buf + o.b8[b] + tm * kARec);
+    }
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++) {
+        const v32f P = __builtin_amdgcn_mfma_f32_32x32x1f32(xs[tn], ys[tm], zero32, 0, 0, 0);
+        const v16f c0 = mx_block_dot(A[0][tn], B[0][tm]);
+        const v16f c1 = mx_block_dot(A[1][tn], B[1][tm]);
+        float t0[16];
+#pragma unroll
+        for (int v = 0; v < 16; v++) t0[v] = fmaf(c0[v], P[v], acc[tn][tm][v]);
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[tn][tm][v] = fmaf(c1[v], P[16 + v], t0[v]);
+      }
+    __builtin_amdgcn_sched_group_barrier(0x100, 5 * (TN + TM), 0);  // DS reads
+#pragma unroll
+    for (int t = 0; t < TN * TM; t++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // outer product + block dots
+      __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);  // folds
+    }
+    return;
+  }
   // The scale outer products go first: lane L holds block L/32, row or token
   // L%32 of the record's f32 scale array [block][row] (read linearly).  Their
   // 16-pass MFMA runs while the dot operands arrive from LDS, and their
@@ -509,6 +549,16 @@ hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, 
   // waves per SIMD: M=512, K=2048, N=10752 (1344 workgroups) takes 43.4 us
   // with the 5-wave form against 41.1 us, M=2048, K=10752, N=2048 (1024) 146
   // against 141.6 us.
+  // 2048 tokens or more without split K: 128-row x 64-token workgroup tiles
+  // (each wave 32 rows x 64 tokens: 156 VGPRs, 3 waves per SIMD, 48 KB of
+  // LDS), 35% fewer operand bytes through L2 and LDS per MAC.  Measured
+  // against the forms below (whole call): M=2048, K=2048, N=10752 141.7 ->
+  // 128.8 us; M=2048, K=10752, N=2048 154.6 -> 141.5 us; M=2048, K=1536,
+  // N=8192 79.2 -> 74.8 us; M=4096, K=2048, N=10752 316 -> 291 us; M=2048,
+  // K=4096, N=4096 unchanged.  Fewer tokens lose (M=256, K=2048, N=10752
+  // 25.8 -> 29.3 us; M=1024, K=10752, N=2048 82.6 -> 94.4 us): half the
+  // workgroups no longer fill the chip.
+  if (splits == 1 && m >= kWideTokens) return launch_cfg<4, 1, 1, 2, 3, 3>(gm, nmat, 1, st);
   if (splits == 1 && gemm_tiles(w, nmat, m) >= kFiveWaveWgs) return launch_cfg<4, 1, 1, 1, 2, 5>(gm, nmat, 1, st);
   return launch_cfg<4, 1, 1, 1, 3, 4>(gm, nmat, splits, st);
 }

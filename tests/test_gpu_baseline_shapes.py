@@ -41,17 +41,19 @@ def test_ragged_gemm_benchmark_shape(gpu_ctx, oracle, m):
 @pytest.mark.parametrize("m,n,k", [(512, 10752, 2048), (512, 2048, 10752), (2048, 10752, 2048),
                                    (2048, 2048, 10752)])
 def test_prefill_gemm_benchmark_shape(gpu_ctx, oracle, m, n, k):
-    """M = 512 (three-buffer form; split-K at K = 10752) and M = 2048 (the two-buffer 5-wave form
-    at K = 2048: 5376 workgroups, 32 block pairs)."""
+    """M = 512 (three-buffer form; split-K at K = 10752) and M = 2048 (128 x 64 workgroup tiles,
+    32 / 168 block pairs)."""
     _gemm_vs_oracle(gpu_ctx, oracle, m, n, k, 400 + m + k)
 
 
 @pytest.mark.parametrize("k", [256, 288])
-def test_five_wave_gemm_steady_state(gpu_ctx, oracle, k):
-    """The two-buffer pipeline refills a buffer after computing it: 4 and 5 block pairs (an even
-    and an odd count) over 5376 workgroups (M = 2048, N = 10752) run its steady state, against
-    the oracle's scalar (reference-order) kernel."""
-    _gemm_vs_oracle(gpu_ctx, oracle, 2048, 10752, k, 500 + k, scalar=True)
+@pytest.mark.parametrize("m", [2048, 2000])
+def test_large_gemm_pipeline_steady_state(gpu_ctx, oracle, m, k):
+    """Past the pipeline fill each stage buffer is refilled after it was computed: 4 and 5 block
+    pairs (an even and an odd count) at N = 10752 run that steady state on the 128 x 64 tile form
+    (M = 2048) and on the two-buffer 5-wave form (M = 2000: 5292 workgroups), against the oracle's
+    scalar (reference-order) kernel."""
+    _gemm_vs_oracle(gpu_ctx, oracle, m, 10752, k, 500 + k + m, scalar=True)
 
 
 @pytest.mark.parametrize("n,k", [(1536, 1536), (8192, 1536), (1536, 8192), (2048, 1536)])
