@@ -22,8 +22,7 @@
 // K advances one block pair per stage.  A stage is the verbatim concatenation
 // of NS weight records and MS activation records (lgh_internal.h), copied
 // global -> LDS by buffer_load ... lds (DMA: no registers, no VALU) into one
-// of three LDS buffers (two for launches of many rounds, which then hold 5
-// waves per SIMD); stages p+1 and p+2 (p+1) are in flight while stage p is
+// of NB LDS buffers; stages p+1 .. p+NB-1 are in flight while stage p is
 // computed, one barrier per stage.
 #include "lgh_device.h"
 #include "lgh_internal.h"
@@ -39,8 +38,7 @@ constexpr int kTile = static_cast<int>(kMxTile);
 constexpr long kSplitTarget = 512;  // two workgroups per CU (M=512, K=10752, N=2048: 61.5 -> 48.6 us vs one)
 constexpr size_t kSplitMinPairs = 64;  // K >= 4096
 constexpr size_t kSplitPairs = 16;     // K >= 1024 per split
-constexpr long kFiveWaveWgs = 5120;  // four rounds of 5 workgroups on each of 256 CUs
-constexpr size_t kWideTokens = 2048;  // 128 x 64 workgroup tiles from this many tokens (no split K)
+constexpr long kWideWgs = 640;  // 128 x 64 workgroup tiles from this many of them (2.5 per CU), no split K
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]
@@ -499,20 +497,17 @@ hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
 
 }  // namespace
 
-// Workgroup tile 128 rows x 32 tokens (4 waves, one 32 x 32 tile each): at
-// every prefill shape measured (M = 512 / 2048, K = 2048 / 10752) it is as
-// fast as or faster than 128 x 64 and 128 x 128 -- the inner loop is bound by
-// the matrix core plus the fold (which do not overlap on gfx950), and the
-// small tile keeps the most workgroups resident to cover the stage loads.
+// Workgroups of a launch with workgroup tiles of NS 32-row x MS 32-token
+// tiles, summed over the matrices of one call.
+template <int NS, int MS>
 static long gemm_tiles(const lgh_q4 *const *w, int nmat, size_t m) {
-  using C = Cfg<4, 1, 1, 1>;
   long tiles = 0;
-  for (int j = 0; j < nmat; j++) tiles += static_cast<long>((w[j]->nt + C::NS - 1) / C::NS);
-  return tiles * static_cast<long>(((m + 31) / 32 + C::MS - 1) / C::MS);
+  for (int j = 0; j < nmat; j++) tiles += static_cast<long>((w[j]->nt + NS - 1) / NS);
+  return tiles * static_cast<long>(((m + 31) / 32 + MS - 1) / MS);
 }
 
 int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m) {
-  return splits_for_tiles<4, 1, 1, 1>(gemm_tiles(w, nmat, m), w[0]->pp);
+  return splits_for_tiles<4, 1, 1, 1>(gemm_tiles<4, 1>(w, nmat, m), w[0]->pp);
 }
 
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
@@ -543,23 +538,20 @@ hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, 
                        static_cast<uint32_t>(mt * w[j]->pp * kMxARec)};
     off += w[j]->n;
   }
-  // Launches of many rounds run the two-buffer pipeline (24 KB of LDS) at 5
-  // waves per SIMD (96 VGPRs): M=2048, K=2048, N=10752 (5376 workgroups)
-  // 144.6-149.6 -> 134.3-137.4 us.  Shorter launches keep three buffers at 4
-  // waves per SIMD: M=512, K=2048, N=10752 (1344 workgroups) takes 43.4 us
-  // with the 5-wave form against 41.1 us, M=2048, K=10752, N=2048 (1024) 146
-  // against 141.6 us.
-  // 2048 tokens or more without split K: 128-row x 64-token workgroup tiles
-  // (each wave 32 rows x 64 tokens: 156 VGPRs, 3 waves per SIMD, 48 KB of
-  // LDS), 35% fewer operand bytes through L2 and LDS per MAC.  Measured
-  // against the forms below (whole call): M=2048, K=2048, N=10752 141.7 ->
-  // 128.8 us; M=2048, K=10752, N=2048 154.6 -> 141.5 us; M=2048, K=1536,
-  // N=8192 79.2 -> 74.8 us; M=4096, K=2048, N=10752 316 -> 291 us; M=2048,
-  // K=4096, N=4096 unchanged.  Fewer tokens lose (M=256, K=2048, N=10752
-  // 25.8 -> 29.3 us; M=1024, K=10752, N=2048 82.6 -> 94.4 us): half the
-  // workgroups no longer fill the chip.
-  if (splits == 1 && m >= kWideTokens) return launch_cfg<4, 1, 1, 2, 3, 3>(gm, nmat, 1, st);
-  if (splits == 1 && gemm_tiles(w, nmat, m) >= kFiveWaveWgs) return launch_cfg<4, 1, 1, 1, 2, 5>(gm, nmat, 1, st);
+  // Without split K and with >= 640 of them: 128-row x 64-token workgroup
+  // tiles (each wave 32 rows x 64 tokens: 156 VGPRs, 3 waves per SIMD, 48 KB
+  // of LDS), 35% fewer operand bytes through L2 and LDS per MAC than 128 x 32.
+  // Whole calls, against 128 x 32: M=512, K=2048, N=10752 (672 workgroups)
+  // 41.3 -> 38.8 us; M=768 / 1024, same K and N, 53.8 -> 52.2 / 71.0 -> 68.6
+  // us; M=2048, K=2048, N=10752 141.7 -> 128.8 us (and against the two-buffer
+  // 5-wave form of 128 x 32, 134-137 us); M=2048, K=1536, N=8192 79.2 -> 74.8
+  // us; M=4096, K=2048, N=10752 316 -> 291 us.  Fewer workgroups leave CUs
+  // idle: M=512, K=2048, N=8192 (512) 32.2 -> 32.5 us, M=256, N=10752 (336)
+  // 25.8 -> 29.3 us, M=1024, K=10752, N=2048 (256; split K otherwise) 82.6
+  // -> 94.4 us.
+  if (splits == 1 && gemm_tiles<4, 2>(w, nmat, m) >= kWideWgs) return launch_cfg<4, 1, 1, 2, 3, 3>(gm, nmat, 1, st);
+  // Otherwise 128 x 32 (4 waves, one 32 x 32 tile each, 108 VGPRs, 4 waves
+  // per SIMD): the most workgroups resident to cover the stage loads.
   return launch_cfg<4, 1, 1, 1, 3, 4>(gm, nmat, splits, st);
 }
 

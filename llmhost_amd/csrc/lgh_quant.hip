@@ -249,7 +249,11 @@ __device__ __forceinline__ void store_hl_group8(uint8_t *rec, int s, int tok, ui
 // of the image is written whole by one workgroup.  The h / l E3M2 codes of
 // each int8 code come from a 256-entry LDS table built per workgroup
 // (q + 128 -> code(h) | code(l) << 6), a lookup in place of ~25 VALU per code.
-constexpr int kActJobs = 2;
+// One half-record per workgroup: whole GEMM calls at M=512, K=2048 / 10752
+// took 41.3 / 50.4 us with two and 42.2 / 50.8 us with four, 40.9 / 49.8 us
+// with one (the kernel is bound by its DRAM round trip; more workgroups
+// keep more of them in flight).
+constexpr int kActJobs = 1;
 
 __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, int m, int bpr,
                                                                 int pp, int per_row,

@@ -1,5 +1,5 @@
 """Parity at the exact shapes the benchmark times, against the oracle's production (VNNI-512)
-kernel, plus the steady state of the two-buffer (5-wave) GEMM pipeline.
+kernel, plus the steady state of both GEMM tile forms' pipelines.
 
 Shapes: the ragged batched GEMMs (M = 4 / 16 / 64, K = 2048, N = 8192), the four prefill GEMMs
 (M = 512 / 2048 x K = 2048, N = 10752 and K = 10752, N = 2048), the decode GEMVs of the headline
@@ -41,18 +41,19 @@ def test_ragged_gemm_benchmark_shape(gpu_ctx, oracle, m):
 @pytest.mark.parametrize("m,n,k", [(512, 10752, 2048), (512, 2048, 10752), (2048, 10752, 2048),
                                    (2048, 2048, 10752)])
 def test_prefill_gemm_benchmark_shape(gpu_ctx, oracle, m, n, k):
-    """M = 512 (three-buffer form; split-K at K = 10752) and M = 2048 (128 x 64 workgroup tiles,
-    32 / 168 block pairs)."""
+    """K = 2048, N = 10752 (128 x 64 workgroup tiles: 672 / 2688 of them at M = 512 / 2048, 32
+    block pairs); K = 10752, N = 2048 (128 x 32 tiles, 168 block pairs: split K at M = 512, 1024
+    workgroups at M = 2048)."""
     _gemm_vs_oracle(gpu_ctx, oracle, m, n, k, 400 + m + k)
 
 
 @pytest.mark.parametrize("k", [256, 288])
-@pytest.mark.parametrize("m", [2048, 2000])
+@pytest.mark.parametrize("m", [2000, 256])
 def test_large_gemm_pipeline_steady_state(gpu_ctx, oracle, m, k):
     """Past the pipeline fill each stage buffer is refilled after it was computed: 4 and 5 block
     pairs (an even and an odd count) at N = 10752 run that steady state on the 128 x 64 tile form
-    (M = 2048) and on the two-buffer 5-wave form (M = 2000: 5292 workgroups), against the oracle's
-    scalar (reference-order) kernel."""
+    (M = 2000, a ragged last token tile) and on 128 x 32 tiles (M = 256: 336 workgroups of
+    128 x 64 would be too few), against the oracle's scalar (reference-order) kernel."""
     _gemm_vs_oracle(gpu_ctx, oracle, m, 10752, k, 500 + k + m, scalar=True)
 
 

@@ -56,13 +56,12 @@ def test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, seed):
     assert_close(got, ref, what=f"m={m} n={n} k={k} mode={mode} per_row={per_row}")
 
 
-# Without split K, launches over 2048 tokens or more take the 128 x 64 workgroup tiles (each
-# wave 32 rows x 64 tokens); below that, launches of >= 5120 workgroups (128-row x 32-token tiles,
-# summed over the matrices of one call) take the two-buffer, 5-waves-per-SIMD form.  Short K keeps
-# the oracle fast; ragged M (a 64-token tile with a missing half), N and an odd block count cover
-# the tile and pair tails.
-WIDE = [(2048, 10752, 64), (2100, 3000, 96), (4096, 700, 128)]
-FIVE_WAVE = [(2000, 10700, 96), (1024, 20600, 64)]
+# Without split K, launches of >= 640 workgroups of 128 rows x 64 tokens (summed over the matrices
+# of one call) take those tiles (each wave 32 rows x 64 tokens); smaller launches keep 128 x 32.
+# Short K keeps the oracle fast; ragged M (a 64-token tile with a missing half), N and an odd
+# block count cover the tile and pair tails.
+WIDE = [(2048, 10752, 64), (2100, 3000, 96), (512, 10752, 96), (770, 10700, 64)]
+NARROW = [(4096, 700, 128), (512, 8192, 96), (300, 10752, 64)]
 
 
 @pytest.mark.parametrize("per_row", [False, True])
@@ -74,12 +73,12 @@ def test_gemm_wide_tile_route(gpu_ctx, oracle, m, n, k, mode, per_row):
 
 @pytest.mark.parametrize("per_row", [False, True])
 @pytest.mark.parametrize("mode", [0, 1, 2])
-@pytest.mark.parametrize("m,n,k", FIVE_WAVE)
-def test_gemm_five_wave_route(gpu_ctx, oracle, m, n, k, mode, per_row):
+@pytest.mark.parametrize("m,n,k", NARROW)
+def test_gemm_below_wide_threshold(gpu_ctx, oracle, m, n, k, mode, per_row):
     test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 31 * m + n + k + mode)
 
 
-@pytest.mark.parametrize("tokens", [2048, 2000])  # wide tiles; the 5-wave form (84 N groups x 63 token tiles)
+@pytest.mark.parametrize("tokens", [2000, 256])  # 128 x 64 tiles (84 N groups x 32); 128 x 32 (84 x 8)
 def test_gemm_large_routes_three_matrices(gpu_ctx, oracle, tokens):
     k, rows = 64, (4096, 4096, 2560)
     bl = [synth.q4_blocks(60 + j, n, k) for j, n in enumerate(rows)]
