@@ -122,9 +122,11 @@ __device__ __forceinline__ i32x4 sgpr_rsrc(const void *base, uint32_t bytes) {
 // Issued as inline asm so that the compiler does not see an LDS write it
 // would have to fence conservatively; the pipeline waits for it explicitly
 // (vmcnt).  voff must stay live (loop-invariant): a VMEM instruction may read
-// its address VGPR after issue.
+// its address VGPR after issue.  An LDS DMA that reads M0 right after an SALU
+// write of M0 needs one wait state on this GPU family (the s_nop; the
+// compiler inserts none inside inline asm).
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds)
                : "memory", "m0");
