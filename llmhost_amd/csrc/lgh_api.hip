@@ -249,6 +249,16 @@ int ensure_mx(lgh_ctx *ctx, const lgh_q4 *wc) {
   return LGH_OK;
 }
 
+// A matrix is used only through a context of the device that holds it.
+template <class M>
+int check_mat(lgh_ctx *ctx, const M *w) {
+  if (int r = check_mat(ctx, w)) return r;
+  if (w->device != ctx->device)
+    return fail(ctx, LGH_ERR_INVALID_ARG, "the matrix is on device %d, the context on device %d", w->device,
+                ctx->device);
+  return LGH_OK;
+}
+
 int check_shape(lgh_ctx *ctx, const void *p, size_t n, size_t k, void *out) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (!out) return fail(ctx, LGH_ERR_INVALID_ARG, "null output handle");
@@ -393,6 +403,7 @@ int lgh_buffer_write(lgh_ctx *ctx, float *dst_dev, const float *src, size_t len)
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (len == 0) return LGH_OK;
   if (!dst_dev || !src) return fail(ctx, LGH_ERR_INVALID_ARG, "null buffer");
+  if (len > SIZE_MAX / sizeof(float)) return fail(ctx, LGH_ERR_SHAPE, "buffer of %zu floats is too large", len);
   if (int r = set_device(ctx)) return r;
   LGH_HIP(ctx, hipMemcpyAsync(dst_dev, src, len * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -403,6 +414,7 @@ int lgh_buffer_read(lgh_ctx *ctx, float *dst, const float *src_dev, size_t len) 
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (len == 0) return LGH_OK;
   if (!dst || !src_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null buffer");
+  if (len > SIZE_MAX / sizeof(float)) return fail(ctx, LGH_ERR_SHAPE, "buffer of %zu floats is too large", len);
   if (int r = set_device(ctx)) return r;
   LGH_HIP(ctx, hipMemcpyAsync(dst, src_dev, len * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
   LGH_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -486,7 +498,7 @@ size_t lgh_q4_image_bytes(const lgh_q4 *w, int with_gemm) {
 
 int lgh_q4_export(lgh_ctx *ctx, const lgh_q4 *w, int with_gemm, void *dst, size_t bytes) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (bytes != lgh_q4_image_bytes(w, with_gemm))
     return fail(ctx, LGH_ERR_SHAPE, "image of %zu x %zu needs %zu bytes, got %zu", w->n, w->k,
                 lgh_q4_image_bytes(w, with_gemm), bytes);
@@ -547,7 +559,7 @@ size_t lgh_q8_image_bytes(const lgh_q8 *w) { return w ? w->n * w->bpr * LGH_BLOC
 
 int lgh_q8_export(lgh_ctx *ctx, const lgh_q8 *w, void *dst, size_t bytes) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (bytes != lgh_q8_image_bytes(w))
     return fail(ctx, LGH_ERR_SHAPE, "image needs %zu bytes, got %zu", lgh_q8_image_bytes(w), bytes);
   if (bytes == 0) return LGH_OK;
@@ -586,7 +598,7 @@ int lgh_q8_import(lgh_ctx *ctx, const void *src, size_t bytes, size_t n, size_t 
 
 int lgh_q4_prepare_gemm(lgh_ctx *ctx, const lgh_q4 *w) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (w->n == 0 || w->bpr == 0) return LGH_OK;
   if (int r = set_device(ctx)) return r;
   return ensure_mx(ctx, w);
@@ -695,7 +707,7 @@ static int launch_gemv(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *w0, float *y0,
 
 int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (int r = check_mode(ctx, mode)) return r;
   if (w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
@@ -706,7 +718,8 @@ int lgh_q4_gemv_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
 int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const float *x_dev, float *yg_dev,
                          float *yu_dev) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!wg || !wu) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, wg)) return r;
+  if (int r = check_mat(ctx, wu)) return r;
   if (wg->k != wu->k || wg->n != wu->n)
     return fail(ctx, LGH_ERR_SHAPE, "pair needs equal shapes: gate %zux%zu, up %zux%zu", wg->n, wg->k, wu->n,
                 wu->k);
@@ -721,7 +734,7 @@ int lgh_q4_gemv_pair_dev(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const
 int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, const float *scales_dev,
                          float *y_dev, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (int r = check_mode(ctx, mode)) return r;
   if (w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && (!qs_dev || !scales_dev))) return fail(ctx, LGH_ERR_INVALID_ARG, "null codes/scales/y");
@@ -752,7 +765,7 @@ int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, co
 
 int lgh_q4_gemv_prep(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, const float *scales, float *y, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (int r = check_mode(ctx, mode)) return r;
   if (w->n == 0) return LGH_OK;
   if (!y || (w->k && (!qs || !scales))) return fail(ctx, LGH_ERR_INVALID_ARG, "null codes/scales/y");
@@ -908,7 +921,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
 
 int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (int r = check_mode(ctx, mode)) return r;
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
@@ -921,7 +934,7 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
 // needs more than the array holds even for 32 tokens fails with LGH_ERR_SHAPE.
 int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (int r = check_mode(ctx, mode)) return r;
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
@@ -932,7 +945,7 @@ int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, f
 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev, size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (tokens == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
@@ -944,7 +957,7 @@ int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_
 int lgh_q8_norm_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w_dev, float eps, const float *hidden_dev,
                          float *y_dev, size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (tokens == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !hidden_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/y");
   if (!aligned16(hidden_dev) || !aligned16(norm_w_dev))
@@ -965,7 +978,7 @@ int lgh_q8_norm_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w_dev,
 int lgh_q8_norm_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *norm_w, float eps, const float *hidden, float *y,
                      size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (tokens == 0 || w->n == 0) return LGH_OK;
   if (!y || (w->k && !hidden)) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden/y");
   if (int r = set_device(ctx)) return r;
@@ -991,7 +1004,7 @@ int lgh_q4_gemv(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, int mod
 
 int lgh_q4_gemm(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, size_t m, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (int r = check_mode(ctx, mode)) return r;
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!x || !y) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
@@ -1013,7 +1026,8 @@ int lgh_q4_gemm(lgh_ctx *ctx, const lgh_q4 *w, const float *x, float *y, size_t 
 int lgh_q4_gemv_pair(lgh_ctx *ctx, const lgh_q4 *wg, const lgh_q4 *wu, const float *x, float *y_gate,
                      float *y_up) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!wg || !wu) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, wg)) return r;
+  if (int r = check_mat(ctx, wu)) return r;
   if (wg->k != wu->k || wg->n != wu->n)
     return fail(ctx, LGH_ERR_SHAPE, "pair needs equal shapes: gate %zux%zu, up %zux%zu", wg->n, wg->k, wu->n,
                 wu->k);
@@ -1094,7 +1108,8 @@ int lgh_silu_mul(lgh_ctx *ctx, float *g, const float *u, size_t n) {
 }
 
 static int check_ffn(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2) {
-  if (!w1 || !w3) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w1)) return r;
+  if (int r = check_mat(ctx, w3)) return r;
   if (w1->k != w3->k || w1->n != w3->n)
     return fail(ctx, LGH_ERR_SHAPE, "gate/up need equal shapes: %zux%zu, %zux%zu", w1->n, w1->k, w3->n, w3->k);
   if (w2 && (w2->k != w1->n || w2->n != w1->k))
@@ -1128,7 +1143,7 @@ static int ffn_fused(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh
 int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
                             const float *norm_w_dev, float eps, float *hidden_dev, size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w2)) return r;
   if (int r = check_ffn(ctx, w1, w3, w2)) return r;
   if (tokens == 0 || w1->k == 0 || w1->n == 0) return LGH_OK;  // nothing, or W2 h = 0 (hidden + 0 is hidden)
   if (!hidden_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
@@ -1157,7 +1172,7 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
 int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2, const float *norm_w,
                         float eps, float *hidden, size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w2) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w2)) return r;
   if (int r = check_ffn(ctx, w1, w3, w2)) return r;
   if (tokens == 0 || w1->k == 0 || w1->n == 0) return LGH_OK;
   if (!hidden) return fail(ctx, LGH_ERR_INVALID_ARG, "null hidden");
@@ -1213,6 +1228,7 @@ static int check_multi(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w) {
   if (!w || nmat < 1 || nmat > 3) return fail(ctx, LGH_ERR_INVALID_ARG, "need 1 to 3 matrices, got %zu", nmat);
   for (size_t j = 0; j < nmat; j++) {
     if (!w[j]) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix %zu", j);
+    if (int r = check_mat(ctx, w[j])) return r;
     if (w[j]->k != w[0]->k)
       return fail(ctx, LGH_ERR_SHAPE, "matrix %zu has k = %zu, matrix 0 k = %zu", j, w[j]->k, w[0]->k);
   }
@@ -1293,7 +1309,7 @@ int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const fl
 
 int lgh_q8_gemv(lgh_ctx *ctx, const lgh_q8 *w, const float *x, float *y, size_t tokens) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (tokens == 0 || w->n == 0) return LGH_OK;
   if (!x || !y) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (int r = set_device(ctx)) return r;
@@ -1383,7 +1399,7 @@ int lgh_q8_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t 
 
 int lgh_q4_mfma_block_dots(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs, size_t m, int32_t *out) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
+  if (int r = check_mat(ctx, w)) return r;
   if (m == 0 || w->n == 0 || w->bpr == 0) return LGH_OK;
   if (!qs || !out) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
   if (int r = set_device(ctx)) return r;
