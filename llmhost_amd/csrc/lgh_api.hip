@@ -252,7 +252,7 @@ int ensure_mx(lgh_ctx *ctx, const lgh_q4 *wc) {
 // A matrix is used only through a context of the device that holds it.
 template <class M>
 int check_mat(lgh_ctx *ctx, const M *w) {
-  if (int r = check_mat(ctx, w)) return r;
+  if (!w) return fail(ctx, LGH_ERR_INVALID_ARG, "null matrix");
   if (w->device != ctx->device)
     return fail(ctx, LGH_ERR_INVALID_ARG, "the matrix is on device %d, the context on device %d", w->device,
                 ctx->device);
