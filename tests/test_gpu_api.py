@@ -147,3 +147,45 @@ def test_trim_releases_workspaces_and_calls_still_work(gpu_ctx, oracle):
     q4.gemm_q4(w, x, b, m)
     assert np.array_equal(a, b)
     w.free()
+
+
+def test_null_matrix_is_an_error_on_every_matrix_entry_point(gpu_ctx):
+    """Each entry point that takes a matrix returns LGH_ERR_INVALID_ARG for a null one (the
+    reference would not compile a missing matrix; here the check runs before any other argument
+    is read, so the remaining pointers may be null too)."""
+    L, h = _ffi.lib(), gpu_ctx.handle
+    w = q4.Q4Matrix.from_blocks(64, 64, synth.q4_blocks(1, 64, 64), gpu_ctx)
+    nul = None
+    calls = {
+        "lgh_q4_export": lambda: L.lgh_q4_export(h, nul, 0, nul, 0),
+        "lgh_q8_export": lambda: L.lgh_q8_export(h, nul, nul, 0),
+        "lgh_q4_prepare_gemm": lambda: L.lgh_q4_prepare_gemm(h, nul),
+        "lgh_q4_gemv": lambda: L.lgh_q4_gemv(h, nul, nul, nul, 0),
+        "lgh_q4_gemv_dev": lambda: L.lgh_q4_gemv_dev(h, nul, nul, nul, 0),
+        "lgh_q4_gemv_pair (gate)": lambda: L.lgh_q4_gemv_pair(h, nul, w.handle, nul, nul, nul),
+        "lgh_q4_gemv_pair (up)": lambda: L.lgh_q4_gemv_pair(h, w.handle, nul, nul, nul, nul),
+        "lgh_q4_gemv_pair_dev": lambda: L.lgh_q4_gemv_pair_dev(h, nul, w.handle, nul, nul, nul),
+        "lgh_q4_gemv_prep": lambda: L.lgh_q4_gemv_prep(h, nul, nul, nul, nul, 0),
+        "lgh_q4_gemv_prep_dev": lambda: L.lgh_q4_gemv_prep_dev(h, nul, nul, nul, nul, 0),
+        "lgh_q4_gemm": lambda: L.lgh_q4_gemm(h, nul, nul, nul, 4, 0),
+        "lgh_q4_gemm_dev": lambda: L.lgh_q4_gemm_dev(h, nul, nul, nul, 4, 0),
+        "lgh_q4_gemm_dev_noalloc": lambda: L.lgh_q4_gemm_dev_noalloc(h, nul, nul, nul, 4, 0),
+        "lgh_q8_gemv": lambda: L.lgh_q8_gemv(h, nul, nul, nul, 1),
+        "lgh_q8_gemv_dev": lambda: L.lgh_q8_gemv_dev(h, nul, nul, nul, 1),
+        "lgh_q8_norm_gemv": lambda: L.lgh_q8_norm_gemv(h, nul, nul, 1e-5, nul, nul, 1),
+        "lgh_q8_norm_gemv_dev": lambda: L.lgh_q8_norm_gemv_dev(h, nul, nul, 1e-5, nul, nul, 1),
+        "lgh_q4_ffn_residual (w2)": lambda: L.lgh_q4_ffn_residual(h, w.handle, w.handle, nul, nul, 1e-5, nul, 1),
+        "lgh_q4_ffn_residual (w1)": lambda: L.lgh_q4_ffn_residual(h, nul, w.handle, w.handle, nul, 1e-5, nul, 1),
+        "lgh_q4_ffn_residual_dev (w3)": lambda: L.lgh_q4_ffn_residual_dev(h, w.handle, nul, w.handle, nul, 1e-5,
+                                                                          nul, 1),
+        "lgh_q4_mfma_block_dots": lambda: L.lgh_q4_mfma_block_dots(h, nul, nul, 1, nul),
+    }
+    try:
+        for name, call in calls.items():
+            assert call() == _ffi.LGH_ERR_INVALID_ARG, name
+            assert b"null matrix" in L.lgh_last_error(h), name
+        mats = (_ffi.C.c_void_p * 2)(w.handle, None)
+        assert L.lgh_q4_norm_gemv(h, 2, mats, nul, 1e-5, nul, nul, 1, 0) == _ffi.LGH_ERR_INVALID_ARG
+        assert b"null matrix 1" in L.lgh_last_error(h)
+    finally:
+        w.free()
