@@ -27,6 +27,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -190,13 +191,15 @@ def gemm_case(gb: GpuBench, m, n, k, iters, seed):
     x = torch.from_numpy(synth.activations(seed + 1, m, k)).cuda()
     y = torch.zeros(m, n, device="cuda")
     C = len(mats)
-    ms = gb.timed(lambda i: q4.gemm_q4(mats[i % C], x, y, m), iters, 3)
+    samples = gb.timed(lambda i: q4.gemm_q4(mats[i % C], x, y, m), iters, 3, reps=5)
+    ms = statistics.median(samples)
     ops = 2.0 * m * n * k
     byts = q4_bytes(n, k, m)
     for w in mats:
         w.free()
     return {"m": m, "n": n, "k": k, "us": ms * 1e3, "tops": ops / (ms * 1e-3) / 1e12,
-            "frac_int8": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "gbs": byts / (ms * 1e-3) / 1e9}
+            "frac_int8": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "gbs": byts / (ms * 1e-3) / 1e9,
+            "samples_us": [round(t * 1e3, 3) for t in samples]}
 
 
 def q8_case(gb: GpuBench, iters, n=1536, k=1536):
