@@ -5,6 +5,7 @@ calls are ones that never touch a device.
 """
 
 import ctypes as C
+import os
 import re
 
 import pytest
@@ -64,3 +65,18 @@ def test_every_gemv_plan_has_a_compiled_kernel():
     """The Q4 and Q8_0 GEMV planners only choose launch shapes the library compiled (a plan
     without a kernel would fail at launch with LGH_ERR_HIP): host-only sweep in the library."""
     assert _ffi.lib().lgh_gemv_plans_uncovered() == 0
+
+
+def test_cpp_header_compiles_and_matches_the_block_formats(tmp_path):
+    """include/llm_gpu_hip.hpp (the C++ host interface) compiles on its own as C++17 with
+    warnings as errors, and its block structs have the reference's sizes (18 / 34 bytes)."""
+    import subprocess
+
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "llm_gpu_hip.hpp"\n'
+                   "static_assert(sizeof(llm_gpu_hip::BlockQ4) == 18, \"q4\");\n"
+                   "static_assert(sizeof(llm_gpu_hip::BlockQ8_0) == 34, \"q8\");\n"
+                   "int main() { return llm_gpu_hip::f16_to_f32(0x3C00) == 1.0f ? 0 : 1; }\n")
+    inc = os.path.dirname(_ffi.HEADER_PATH)
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-I", inc, str(src)],
+                   check=True)
