@@ -407,7 +407,7 @@ def decode_step_case(gb: GpuBench, iters, layers=16, dim=1536, inter=8192, vocab
 
 def cpu_available() -> int:
     """CPUs this process may run on: its affinity mask, bounded by a cgroup CPU quota when one is
-    set (a GPU box's share of a larger host)."""
+    set (a container's share of a larger host)."""
     n = len(os.sched_getaffinity(0))
     try:
         with open("/sys/fs/cgroup/cpu.max") as f:

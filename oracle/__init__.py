@@ -5,7 +5,7 @@ ctypes binding of ``oracle/liboracle.so``, a C restatement of
 Q8_0 head GEMV in ``crates/llm-engine/src/weights.rs:194-227``.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package: as the checker the GPU path is compared
+``bench.py`` may import this package: as the reference the GPU path is compared
 against, and as the timed CPU baseline.  The product package ``llmhost_amd``
 never imports it.
 """

@@ -3,7 +3,7 @@
  *
  * A C restatement of crates/llm-quant/src/lib.rs, crates/llm-cpu/src/
  * gemv_q4.rs (+ pool.rs thread split) and crates/llm-engine/src/weights.rs
- * q8_apply.  Used only by tests (as the checker), by the GPU smoke check and
+ * q8_apply.  Used only by tests (as the reference results), by the GPU smoke check and
  * as bench.py's timed CPU baseline.  The product library never links it.
  *
  * Floating-point contract: this file is compiled with -ffp-contract=off so

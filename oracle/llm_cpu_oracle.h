@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  This is a C restatement of llmhost's CPU
  * algorithm (crates llm-quant and llm-cpu, plus the Q8_0 head GEMV in
  * llm-engine).  Only tests/, __graft_entry__.smoke() and the cpu_baseline
- * leg of bench.py may load it, and only as the checker or as the reported
+ * leg of bench.py may load it, and only as the reference results or as the reported
  * CPU baseline.  The GPU library never links or calls it.
  *
  * Every function cites the reference file:line it restates (paths relative

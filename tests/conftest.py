@@ -13,7 +13,7 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
-# Output tolerance of the north-star gate: |gpu - cpu| <= 1e-4 + 1e-5 * |cpu|.
+# Output tolerance against llm-cpu (only summation order differs): |gpu - cpu| <= 1e-4 + 1e-5 * |cpu|.
 ATOL = 1e-4
 RTOL = 1e-5
 

@@ -3,7 +3,7 @@
   * lgh_q4_norm_gemv: rms_norm of hidden, then 1..3 projections sharing K (Lfm2::attn_decode's
     q/k/v, crates/llm-engine/src/lfm2.rs:784-794; Lfm2::conv_update's in_proj, lfm2.rs:651-659).
     Against the oracle's rms_norm followed by its scalar-order GEMV (the reference operation
-    order) within the north-star tolerance, and bit for bit against the library's own op
+    order) within the output tolerance (1e-4 + 1e-5 |ref|), and bit for bit against the library's own op
     sequence (lgh_rms_norm, then one lgh_q4_gemm per matrix) -- the one-launch form shares one
     activation quantization and must not change a single output bit.
   * LGH_ADD_F32 (Linear::apply then ops::add_inplace, crates/llm-cpu/src/ops.rs:48-53, after
