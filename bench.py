@@ -473,8 +473,8 @@ def cpu_timed(fn, target_s: float):
 
 
 def cpu_baseline(target_s: float = 10.0, row_s: float = 4.0):
-    """The oracle's llm-cpu restatement (runtime-dispatched kernel: VNNI-512 > AVX2 > scalar,
-    pinned pool of pool.rs) on this host, on 1 thread and on every available core (capped at
+    """The oracle's llm-cpu restatement (runtime-dispatched kernel: VNNI-512 > AVX2 > scalar, AMX
+    tiles for the GEMM where the host has them; pinned pool of pool.rs) on this host, on 1 thread and on every available core (capped at
     pool.rs's 64), over rotating packed copies larger than the LLC: the headline GEMV step (the
     returned row), and rows for the M=512 prefill GEMM and the 16-layer decode sweep."""
     import oracle
@@ -519,12 +519,14 @@ def cpu_baseline(target_s: float = 10.0, row_s: float = 4.0):
     gm = [oracle.Q4Matrix(n, k, blocks) for _ in range(4)]
     x = synth.activations(913, m, k)
     out = np.zeros((m, n), dtype=np.float32)
+    # gemm_q4_mode (gemv_q4.rs:711) takes the AMX-INT8 tiles on a host that has them
+    gemm_kern = oracle.kernel_name(oracle.KERNEL_AMX if oracle.amx_ready() else kern)
     for threads in (1, cores):
         oracle.gemm_q4(gm[0], x, m, out=out, threads=threads)
         calls, el, noise = cpu_timed(lambda i, t=threads: oracle.gemm_q4(gm[i % 4], x, m, out=out, threads=t), row_s)
         tops = calls * 2.0 * m * n * k / el / 1e12
         rows.append({"workload": f"Q4 GEMM M={m} K={k} N={n}", "threads": threads, "value": round(tops, 4),
-                     "unit": "TOPS", "ms_per_call": round(el / calls * 1e3, 3), "calls": calls,
+                     "unit": "TOPS", "kernel": gemm_kern, "ms_per_call": round(el / calls * 1e3, 3), "calls": calls,
                      "seconds": round(el, 2), **noise})
     del gm
 

@@ -27,6 +27,7 @@ BLOCK_Q8 = np.dtype([("scale", "<u2"), ("qs", "i1", (32,))])
 assert BLOCK_Q4.itemsize == 18 and BLOCK_Q8.itemsize == 34
 
 KERNEL_DETECT, KERNEL_SCALAR, KERNEL_AVX2, KERNEL_VNNI = -1, 0, 1, 2
+KERNEL_AMX = 3  # GEMM only (m >= 16, no add): llm-cpu/src/amx.rs
 
 _lib = None
 
@@ -74,6 +75,7 @@ def lib():
         L.oq_ffn_residual.argtypes = [P, P, P, P, C.c_float, P, sz, i, i, i]
         L.oq_thread_range.argtypes = [sz, sz, sz, C.POINTER(sz), C.POINTER(sz)]
         L.oq_cpu_has.argtypes, L.oq_cpu_has.restype = [C.c_char_p], i
+        L.oq_amx_ready.restype = i
         _lib = L
     return _lib
 
@@ -272,7 +274,14 @@ def detect_kernel() -> int:
 
 
 def kernel_name(k: int) -> str:
-    return {KERNEL_SCALAR: "scalar", KERNEL_AVX2: "avx2", KERNEL_VNNI: "vnni512"}[k]
+    return {KERNEL_SCALAR: "scalar", KERNEL_AVX2: "avx2", KERNEL_VNNI: "vnni512", KERNEL_AMX: "amx-int8"}[k]
+
+
+def amx_ready() -> bool:
+    """amx_ready (llm-cpu/src/amx.rs:29-66): the CPU has AMX-TILE and AMX-INT8 and the process
+    may use tile data.  gemm_q4 with the detected kernel then takes the AMX tiles for m >= 16
+    without add (gemv_q4.rs:711)."""
+    return bool(lib().oq_amx_ready())
 
 
 def thread_range(tid: int, nthreads: int, n: int):

@@ -14,6 +14,7 @@
 #define _GNU_SOURCE
 #include "llm_cpu_oracle.h"
 
+#include <cpuid.h>
 #include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
@@ -21,6 +22,7 @@
 #include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/syscall.h>
 #include <unistd.h>
 
 /* ======================================================================
@@ -731,10 +733,170 @@ __attribute__((target("avx512f,avx512bw,avx512vnni"))) static void gemm_tiles_vn
   free(acc);
 }
 
+/* ======================================================================
+ * AMX-INT8 GEMM tiles: llm-cpu/src/amx.rs.  gemm_q4_mode takes them for
+ * m >= 16 without add when the host can run AMX (gemv_q4.rs:711).
+ * amx_ready (amx.rs:29-66): CPUID AMX-TILE and AMX-INT8, then Linux
+ * arch_prctl(ARCH_REQ_XCOMP_PERM, XTILEDATA) once per process.  Palette
+ * (amx.rs:79-106): tmm0/1 B panels 8 x 64 bytes (VNNI: row r holds K
+ * 4r..4r+3 of each of 16 columns), tmm2/3 A 16 tokens x 32 codes, tmm4-7 C
+ * 16 x 16 i32.  Per K block (amx.rs:329-518): A = the block's codes of every
+ * token (zero rows to a multiple of 16); for N-tile pairs and 32-token steps,
+ * C = A x B by tdpbssd, stored and folded into an f32 accumulator --
+ * fma(f32(c), sw * sa, acc) for a whole 16-column tile, acc + (c * sw) * sa
+ * for a partial one (fold_c / fold_c_avx512, amx.rs:264-320).
+ * ==================================================================== */
+static atomic_int g_amx_state; /* 0 unknown, 1 ready, 2 not available */
+
+static int amx_probe(void) {
+  unsigned a, b, c, d;
+  if (!__get_cpuid_count(7, 0, &a, &b, &c, &d)) return 0;
+  const int tile = (d >> 24) & 1, int8 = (d >> 25) & 1;
+  if (!tile || !int8) return 0;
+  /* ARCH_REQ_XCOMP_PERM = 0x1023, XFEATURE_XTILEDATA = 18 */
+  return syscall(SYS_arch_prctl, 0x1023, 18) == 0;
+}
+
+int oq_amx_ready(void) {
+  int st = atomic_load_explicit(&g_amx_state, memory_order_acquire);
+  if (st == 0) {
+    st = amx_probe() ? 1 : 2;
+    atomic_store_explicit(&g_amx_state, st, memory_order_release);
+  }
+  return st == 1;
+}
+
+struct amx_tilecfg {
+  uint8_t palette_id, start_row, reserved[14];
+  uint16_t colsb[16];
+  uint8_t rows[16];
+} __attribute__((aligned(64)));
+
+static __thread int t_amx_cfg_loaded;
+
+__attribute__((target("amx-tile,amx-int8"))) static void amx_load_cfg(void) {
+  if (t_amx_cfg_loaded) return;
+  struct amx_tilecfg cfg;
+  memset(&cfg, 0, sizeof cfg);
+  cfg.palette_id = 1;
+  for (int t = 0; t < 2; t++) cfg.rows[t] = 8, cfg.colsb[t] = 64;   /* B */
+  for (int t = 2; t < 4; t++) cfg.rows[t] = 16, cfg.colsb[t] = 32;  /* A */
+  for (int t = 4; t < 8; t++) cfg.rows[t] = 16, cfg.colsb[t] = 64;  /* C */
+  _tile_loadconfig(&cfg);
+  t_amx_cfg_loaded = 1;
+}
+
+/* The tile panel's nibbles as the signed int8 B panel: byte j of column c
+ * in pair p (panel + 64p + 4c + j) holds K 8p+j (low nibble, row 2p) and
+ * K 8p+4+j (high nibble, row 2p+1), each stored +8 (amx.rs:229-244). */
+static void amx_pack_b(const uint8_t *panel, int8_t dst[8 * 64]) {
+  for (int pair = 0; pair < 4; pair++)
+    for (int i = 0; i < 64; i++) {
+      const uint8_t b = panel[pair * 64 + i];
+      dst[(2 * pair) * 64 + i] = (int8_t)((int)(b & 0x0f) - 8);
+      dst[(2 * pair + 1) * 64 + i] = (int8_t)((int)(b >> 4) - 8);
+    }
+}
+
+__attribute__((target("avx512f"))) static void amx_fold(const int32_t c[16 * 16], float *acc, size_t acc_stride,
+                                                        size_t tok, size_t rows, size_t cols, size_t col_off,
+                                                        const float sw[16], const float *scales, size_t kb,
+                                                        size_t bpr) {
+  if (cols == OQ_TILE_N) {
+    const __m512 vsw = _mm512_loadu_ps(sw);
+    for (size_t r = 0; r < rows; r++) {
+      const float sa = scales[(tok + r) * bpr + kb];
+      float *dst = acc + (tok + r) * acc_stride + col_off;
+      const __m512 vc = _mm512_cvtepi32_ps(_mm512_loadu_si512((const void *)(c + r * 16)));
+      _mm512_storeu_ps(dst, _mm512_fmadd_ps(vc, _mm512_mul_ps(vsw, _mm512_set1_ps(sa)), _mm512_loadu_ps(dst)));
+    }
+    return;
+  }
+  for (size_t r = 0; r < rows; r++) {
+    const float sa = scales[(tok + r) * bpr + kb];
+    float *dst = acc + (tok + r) * acc_stride + col_off;
+    for (size_t col = 0; col < cols; col++) dst[col] += (float)c[r * 16 + col] * sw[col] * sa;
+  }
+}
+
+__attribute__((target("amx-tile,amx-int8,avx512f"))) static void gemm_tiles_amx(
+    const oq_q4_matrix *w, const int8_t *qs, const float *scales, float *out, size_t m, size_t t0, size_t t1) {
+  if (t0 >= t1 || m == 0) return;
+  amx_load_cfg();
+  const size_t n = w->n, k = w->k, bpr = k / OQ_BLOCK;
+  const size_t acc_stride = (t1 - t0) * OQ_TILE_N, m_pad = (m + 15) / 16 * 16;
+  float *acc = calloc(m * acc_stride, sizeof(float));
+  int8_t *a_pack = aligned_alloc(64, m_pad * 32);
+  int32_t c0[16 * 16] __attribute__((aligned(64))), c1[16 * 16] __attribute__((aligned(64)));
+  int8_t b0[8 * 64] __attribute__((aligned(64))), b1[8 * 64] __attribute__((aligned(64)));
+  float sw0[16], sw1[16];
+  for (size_t kb = 0; kb < bpr; kb++) {
+    memset(a_pack, 0, m_pad * 32);
+    for (size_t t = 0; t < m; t++) memcpy(a_pack + t * 32, qs + t * k + kb * OQ_BLOCK, 32);
+    size_t col_base = 0;
+    for (size_t tile = t0; tile < t1;) {
+      const int two = tile + 1 < t1;
+      const size_t row0 = tile * OQ_TILE_N;
+      const size_t cols0 = n > row0 ? (n - row0 < 16 ? n - row0 : 16) : 0;
+      const size_t cols1 = two ? (n > row0 + 16 ? (n - row0 - 16 < 16 ? n - row0 - 16 : 16) : 0) : 0;
+      const uint8_t *p0 = w->tiles + (tile * bpr + kb) * OQ_TILE_STRIDE;
+      const uint8_t *p1 = two ? w->tiles + ((tile + 1) * bpr + kb) * OQ_TILE_STRIDE : NULL;
+      for (int col = 0; col < 16; col++) sw0[col] = tile_scale(p0, col);
+      amx_pack_b(p0, b0);
+      _tile_loadd(0, b0, 64);
+      if (two) {
+        for (int col = 0; col < 16; col++) sw1[col] = tile_scale(p1, col);
+        amx_pack_b(p1, b1);
+        _tile_loadd(1, b1, 64);
+      }
+      for (size_t tok = 0; tok < m; tok += 32) {
+        const size_t rows0 = m - tok < 16 ? m - tok : 16;
+        const size_t rows1 = m - tok > 16 ? (m - tok - 16 < 16 ? m - tok - 16 : 16) : 0;
+        _tile_zero(4);
+        _tile_loadd(2, a_pack + tok * 32, 32);
+        _tile_dpbssd(4, 2, 0);
+        _tile_stored(4, c0, 64);
+        if (two) {
+          _tile_zero(5);
+          _tile_dpbssd(5, 2, 1);
+          _tile_stored(5, c1, 64);
+        }
+        amx_fold(c0, acc, acc_stride, tok, rows0, cols0, col_base, sw0, scales, kb, bpr);
+        if (two) amx_fold(c1, acc, acc_stride, tok, rows0, cols1, col_base + 16, sw1, scales, kb, bpr);
+        if (rows1) {
+          _tile_zero(6);
+          _tile_loadd(3, a_pack + (tok + 16) * 32, 32);
+          _tile_dpbssd(6, 3, 0);
+          _tile_stored(6, c0, 64);
+          if (two) {
+            _tile_zero(7);
+            _tile_dpbssd(7, 3, 1);
+            _tile_stored(7, c1, 64);
+          }
+          amx_fold(c0, acc, acc_stride, tok + 16, rows1, cols0, col_base, sw0, scales, kb, bpr);
+          if (two) amx_fold(c1, acc, acc_stride, tok + 16, rows1, cols1, col_base + 16, sw1, scales, kb, bpr);
+        }
+      }
+      col_base += two ? 32 : 16;
+      tile += two ? 2 : 1;
+    }
+  }
+  for (size_t ti = 0; ti < t1 - t0; ti++) {
+    const size_t row0 = (t0 + ti) * OQ_TILE_N;
+    const size_t cols = n > row0 ? (n - row0 < 16 ? n - row0 : 16) : 0;
+    for (size_t t = 0; t < m; t++)
+      for (size_t col = 0; col < cols; col++) out[t * n + row0 + col] = acc[t * acc_stride + ti * 16 + col];
+  }
+  free(a_pack);
+  free(acc);
+}
+
 static void gemm_range(void *c, size_t tid, size_t t0, size_t t1) {
   (void)tid;
   struct gemm_job *j = c;
-  if (j->kernel == OQ_KERNEL_VNNI && has_vnni512())
+  if (j->kernel == OQ_KERNEL_AMX)
+    gemm_tiles_amx(j->w, j->qs, j->scales, j->out, j->m, t0, t1);
+  else if (j->kernel == OQ_KERNEL_VNNI && has_vnni512())
     gemm_tiles_vnni512(j->w, j->qs, j->scales, j->out, j->m, t0, t1, j->add);
   else
     gemm_tiles_scalar(j->w, j->qs, j->scales, j->out, j->m, t0, t1, j->add);
@@ -758,7 +920,14 @@ void oq_gemm_q4(const oq_q4_matrix *w, const float *x, float *out, size_t m, int
   size_t k = w->k, bpr = k / OQ_BLOCK;
   int8_t *qs = malloc(m * k);
   float *sc = malloc(m * bpr * sizeof(float));
-  struct gemm_job j = {w, qs, sc, out, m, resolve_kernel(kernel), add, per_row, x, qs, sc};
+  /* gemv_q4.rs:711: AMX for m >= 16 without add on an AMX host (detected
+   * kernel), or when asked for; else the tile kernels. */
+  int kern = kernel;
+  if ((kernel < 0 || kernel == OQ_KERNEL_AMX) && m >= 16 && !add && oq_amx_ready())
+    kern = OQ_KERNEL_AMX;
+  else
+    kern = resolve_kernel(kernel == OQ_KERNEL_AMX ? -1 : kernel);
+  struct gemm_job j = {w, qs, sc, out, m, kern, add, per_row, x, qs, sc};
   for_ranges((size_t)threads, m, quant_range, &j);
   for_ranges((size_t)threads, w->n_tiles, gemm_range, &j);
   free(qs);

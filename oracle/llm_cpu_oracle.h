@@ -39,7 +39,8 @@ typedef struct {
 } oq_block_q8;
 
 /* Kernel selector, llm-cpu/src/gemv_q4.rs:302-307 Q4Kernel. */
-enum { OQ_KERNEL_SCALAR = 0, OQ_KERNEL_AVX2 = 1, OQ_KERNEL_VNNI = 2 };
+enum { OQ_KERNEL_SCALAR = 0, OQ_KERNEL_AVX2 = 1, OQ_KERNEL_VNNI = 2,
+       OQ_KERNEL_AMX = 3 /* GEMM only: amx.rs gemm_tiles_amx (m >= 16, no add) */ };
 
 /* ---- f16 (half 2.7.1 f16::to_f32 / from_f32: exact / round-nearest-even) */
 float oq_f16_to_f32(uint16_t h);
@@ -89,7 +90,10 @@ void oq_gemv_q4_prep(const oq_q4_matrix *w, const int8_t *qs, const float *scale
 /* gemv_q4_pair (gemv_q4.rs:396-443). */
 void oq_gemv_q4_pair(const oq_q4_matrix *wg, const oq_q4_matrix *wu, const float *x,
                      float *out_g, float *out_u, int per_row, int kernel, int threads);
-/* gemm_q4 / gemm_q4_add (gemv_q4.rs:686-722), without the AMX branch. */
+/* gemm_q4 / gemm_q4_add (gemv_q4.rs:686-722).  With kernel -1 (detected) or
+ * OQ_KERNEL_AMX, m >= 16 and no add take the AMX-INT8 tiles when the host
+ * can run them (amx.rs; gemv_q4.rs:711); otherwise the tile kernels. */
+int oq_amx_ready(void); /* amx.rs:29-66: CPU and OS can run AMX-INT8 tiles */
 void oq_gemm_q4(const oq_q4_matrix *w, const float *x, float *out, size_t m, int add,
                 int per_row, int kernel, int threads);
 /* q8_apply (llm-engine/src/weights.rs:194-227): blocks row-major [n][k/32]. */

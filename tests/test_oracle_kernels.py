@@ -244,6 +244,83 @@ def test_gemm_closed_form_and_add(oracle, per_row):
     assert np.array_equal(got, (y0.astype(np.float64) + g.astype(np.float64)).astype(np.float32))
 
 
+# ---- AMX-INT8 tiles (crates/llm-cpu/src/amx.rs) --------------------------------------------------
+@pytest.fixture
+def amx_host(oracle):
+    if not oracle.amx_ready():
+        pytest.skip("the host cannot run AMX-INT8 tiles (no AMX-INT8 in CPUID, or the kernel "
+                    "refused the tile-data permission)")
+
+
+@pytest.mark.usefixtures("amx_host")
+def test_amx_gemm_matches_gemv(oracle):
+    """amx_gemm_matches_gemv_when_available (amx.rs:526-557): n=48, k=64, m=40, two threads."""
+    n, k, m = 48, 64, 40
+    w = ((((np.arange(n * k) * 3) % 17) - 8).astype(np.float32) * np.float32(0.1)).astype(np.float32)
+    x = ((((np.arange(m * k) * 5) % 11) - 5).astype(np.float32) * np.float32(0.2)).astype(np.float32)
+    mat = oracle.Q4Matrix.from_f32(w, n, k)
+    gemm = oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_AMX, threads=2)
+    gemv = np.stack([oracle.gemv_q4(mat, x[t * k:(t + 1) * k]) for t in range(m)])
+    assert np.all(np.abs(gemm - gemv) <= 1e-4 * (1 + np.abs(gemv)))
+
+
+@pytest.mark.usefixtures("amx_host")
+@pytest.mark.parametrize("threads", [1, 4])
+@pytest.mark.parametrize("m,n,k", [(16, 64, 64), (17, 96, 96), (40, 48, 2048), (100, 160, 288), (33, 32, 1536)])
+def test_amx_equals_vnni_on_whole_tiles(oracle, m, n, k, threads):
+    """On 16-column tiles the AMX fold is fma(f32(c), sw * sa, acc) per block in ascending order,
+    the VNNI kernel's own operation (fold_c_avx512, amx.rs:293-320; gemv_q4.rs:930-936): the two
+    agree bit for bit, and match the exact float64 reference within the output tolerance."""
+    if not oracle.cpu_has("avx512vnni"):
+        pytest.skip("no VNNI-512 kernel to compare with")
+    blocks = synth.q4_blocks(700 + m + n + k, n, k)
+    x = synth.activations(701 + m, m, k)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    amx = oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_AMX, threads=threads)
+    vnni = oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_VNNI, threads=threads)
+    assert np.array_equal(amx.view(np.uint32), vnni.view(np.uint32))
+    qs, sc, _ = oracle.act_quantize(x, False)
+    ref = np.stack([_gemv_f64(blocks, n, k, qs[t], sc[t]) for t in range(m)])
+    assert_close(amx, ref, what="amx vs exact")
+
+
+@pytest.mark.usefixtures("amx_host")
+@pytest.mark.parametrize("m,n,k", [(16, 17, 64), (50, 1000, 128), (31, 70, 192)])
+def test_amx_partial_tiles_within_tolerance(oracle, m, n, k):
+    """A partial last tile (n % 16 != 0) folds as acc + (c * sw) * sa (fold_c, amx.rs:280-288):
+    within the output tolerance of the exact reference, and equal to VNNI on the whole tiles."""
+    blocks = synth.q4_blocks(710 + m + n, n, k)
+    x = synth.activations(711 + m, m, k)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    amx = oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_AMX, threads=2)
+    qs, sc, _ = oracle.act_quantize(x, False)
+    ref = np.stack([_gemv_f64(blocks, n, k, qs[t], sc[t]) for t in range(m)])
+    assert_close(amx, ref, what="amx partial tiles")
+    whole = n // 16 * 16
+    if whole and oracle.cpu_has("avx512vnni"):
+        vnni = oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_VNNI, threads=2)
+        assert np.array_equal(amx[:, :whole].view(np.uint32), vnni[:, :whole].view(np.uint32))
+
+
+@pytest.mark.usefixtures("amx_host")
+def test_amx_dispatch_follows_gemm_q4_mode(oracle):
+    """gemv_q4.rs:711: the detected kernel takes AMX for m >= 16 without add; m = 15, and
+    gemm_q4_add at any m, stay on the tile kernels."""
+    n, k = 40, 96  # a partial last tile, where AMX and VNNI round differently
+    blocks = synth.q4_blocks(720, n, k)
+    mat = oracle.Q4Matrix(n, k, blocks)
+    for m, want in ((16, oracle.KERNEL_AMX), (15, oracle.KERNEL_VNNI)):
+        x = synth.activations(721 + m, m, k)
+        auto = oracle.gemm_q4(mat, x, m, kernel=oracle.KERNEL_DETECT)
+        forced = oracle.gemm_q4(mat, x, m, kernel=want)
+        assert np.array_equal(auto.view(np.uint32), forced.view(np.uint32)), m
+    x = synth.activations(730, 20, k)
+    y0 = synth.activations(731, 20, n)
+    add = oracle.gemm_q4(mat, x, 20, out=y0.copy(), add=True)
+    tile = oracle.gemm_q4(mat, x, 20, kernel=oracle.KERNEL_VNNI)
+    assert np.array_equal(add, (y0.astype(np.float64) + tile.astype(np.float64)).astype(np.float32))
+
+
 # ---- Q8_0 GEMV (weights.rs:194-227) ------------------------------------------------------------
 def test_q8_apply_closed_form(oracle):
     n, k, tokens = 77, 256, 3
