@@ -310,7 +310,8 @@ int lgh_q4_ffn_gate_up(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const f
 /* Host-only check of the kernel dispatch (no device needed): the number of
  * GEMV launch shapes the planner can choose, over a sweep of row counts
  * around every planner threshold, every K up to 32768 and 1-3 matrices, that
- * have no compiled Q4 / Q8_0 kernel.  0 means every plan can launch. */
+ * have no compiled Q4 / Q8_0 kernel, plus the ragged matrix-core kernel's
+ * plans for 2-64 tokens.  0 means every plan can launch. */
 int lgh_gemv_plans_uncovered(void);
 /* Integer Q8_0 x Q8 block dot (crates/llm-engine/src/weights.rs:206-209). */
 int lgh_q8_block_dots(lgh_ctx *ctx, const void *blocks, const int8_t *a, size_t nblocks,

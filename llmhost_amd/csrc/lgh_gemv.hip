@@ -31,6 +31,13 @@ namespace lgh {
   X(4, 1, 16) X(4, 1, 8) X(4, 1, 4) X(1, 2, 4) X(2, 2, 4) X(4, 2, 16) X(2, 4, 16) X(2, 4, 8) X(2, 4, 4)  \
   X(4, 4, 16) X(2, 8, 16) X(2, 8, 8) X(4, 8, 16) X(2, 16, 16) X(4, 16, 16)
 
+// (TT, KW, CB, RG) of every ragged MMA kernel shape plan_q4_mma can choose;
+// the dispatch is generated from this list too.
+#define LGH_MMA_SHAPES(X)                                                                           \
+  X(1, 1, 8, 4) X(1, 2, 8, 2) X(1, 4, 8, 1) X(1, 8, 8, 1) X(2, 1, 8, 4) X(2, 2, 8, 2) X(2, 4, 8, 1) \
+  X(2, 8, 8, 1) X(3, 1, 8, 4) X(3, 2, 8, 2) X(3, 4, 8, 1) X(3, 8, 8, 1) X(3, 8, 4, 1) X(4, 1, 8, 4) \
+  X(4, 2, 8, 2) X(4, 4, 8, 1) X(4, 8, 8, 1)
+
 namespace {
 
 
@@ -833,6 +840,14 @@ Q4GemvPlan plan_q4_gemv(size_t n, size_t bpr, int nmat, bool narrow) {
   return p;
 }
 
+bool mma_shape_compiled(int tt, int kw, int cb, int rg) {
+#define LGH_HAS(T_, K_, C_, R_) \
+  if (tt == T_ && kw == K_ && cb == C_ && rg == R_) return true;
+  LGH_MMA_SHAPES(LGH_HAS)
+#undef LGH_HAS
+  return false;
+}
+
 bool gemv_shape_compiled(int bpl, int kw, int w) {
 #define LGH_HAS(BB, KK, WW) \
   if (bpl == BB && kw == KK && w == WW) return true;
@@ -863,6 +878,15 @@ int gemv_plans_uncovered() {
           check(n);
           check(3 * n);
         }
+      }
+  // The ragged MMA planner: every token count it takes, row lengths 1..1024
+  // blocks, row counts on both sides of its 8192-row and 16384-row tests.
+  for (size_t m = 1; m <= 65; m++)
+    for (size_t bpr = 1; bpr <= 1024; bpr++)
+      for (size_t n : {size_t{1}, size_t{16}, size_t{8191}, size_t{8192}, size_t{8193}, size_t{16383},
+                       size_t{16384}, size_t{16385}, size_t{1} << 20}) {
+        const Q4MmaPlan p = plan_q4_mma(n, m, bpr);
+        if (p.ok && !mma_shape_compiled(p.TT, p.KW, p.CB, p.RG)) missing++;
       }
   return missing;
 }
@@ -1010,6 +1034,14 @@ Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr) {
   if (m > 48 && (bpr >= 256 || (bpr >= 128 && n >= 16384))) return p;
   p.TT = static_cast<int>((m + 15) / 16);
   p.CB = 8;
+  // Three token tiles over rows of >= 48 blocks and up to 8192 rows: 4-block
+  // chunks over 8 K slices (two chunks per wave, 127 VGPRs: the 4 waves per
+  // SIMD of up to 512 workgroups are resident at once) instead of 8-block
+  // chunks over 4.  M=40 / 48, whole call: K=1536, N=1536 / 2048 9.1 -> 7.8 /
+  // 8.0 us; K=2048, N=8192 11.9 -> 11.7 / 11.6 us; K=4096, N=4096 12.2 ->
+  // 11.4 us; K=8192, N=1536 17.3 -> 16.1 us.  At N=16384 (two rounds of
+  // waves) it was slower: 17.9 -> 19.0 us.
+  if (p.TT == 3 && bpr >= 48 && n <= 8192) p.CB = 4;
   const size_t nch = (bpr + p.CB - 1) / p.CB;
   const size_t per_wave = p.TT >= 3 ? 2 : 1;
   p.KW = 1;
@@ -1026,23 +1058,8 @@ hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float
   Q4MmaArgs a{w->qs, w->sc, codes, scales, y, static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(m),
               mode, static_cast<int>((m + 15) / 16), static_cast<int>((w->bpr + 3) / 4)};
 #define LGH_M(TT_, KW_, CB_, RG_) \
-  if (p.TT == TT_ && p.KW == KW_ && p.CB == CB_ && p.RG == RG_) return launch_mma<TT_, KW_, CB_, RG_>(a, st)
-  LGH_M(1, 1, 8, 4);
-  LGH_M(1, 2, 8, 2);
-  LGH_M(1, 4, 8, 1);
-  LGH_M(1, 8, 8, 1);
-  LGH_M(2, 1, 8, 4);
-  LGH_M(2, 2, 8, 2);
-  LGH_M(2, 4, 8, 1);
-  LGH_M(2, 8, 8, 1);
-  LGH_M(3, 1, 8, 4);
-  LGH_M(3, 2, 8, 2);
-  LGH_M(3, 4, 8, 1);
-  LGH_M(3, 8, 8, 1);
-  LGH_M(4, 1, 8, 4);
-  LGH_M(4, 2, 8, 2);
-  LGH_M(4, 4, 8, 1);
-  LGH_M(4, 8, 8, 1);
+  if (p.TT == TT_ && p.KW == KW_ && p.CB == CB_ && p.RG == RG_) return launch_mma<TT_, KW_, CB_, RG_>(a, st);
+  LGH_MMA_SHAPES(LGH_M)
 #undef LGH_M
   return hipErrorInvalidValue;
 }

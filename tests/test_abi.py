@@ -62,8 +62,9 @@ def test_init_reports_missing_device_or_wrong_arch():
 
 
 def test_every_gemv_plan_has_a_compiled_kernel():
-    """The Q4 and Q8_0 GEMV planners only choose launch shapes the library compiled (a plan
-    without a kernel would fail at launch with LGH_ERR_HIP): host-only sweep in the library."""
+    """The Q4 and Q8_0 GEMV planners and the ragged (2-64 token) matrix-core planner only choose
+    launch shapes the library compiled (a plan without a kernel would fail at launch with
+    LGH_ERR_HIP): host-only sweep in the library."""
     assert _ffi.lib().lgh_gemv_plans_uncovered() == 0
 
 
