@@ -280,7 +280,10 @@ inline void gemv_q4_prep(const Q4Matrix &w, const ActQ8 &a, std::vector<float> &
                                                 out.data(), LGH_ASSIGN));
 }
 
-// gemv_q4_pair (gemv_q4.rs:396-443): gate and up on one activation.
+// gemv_q4_pair (gemv_q4.rs:396-443): gate and up on one activation.  The
+// reference asserts equal k and equal 16-row tile counts and stores both
+// outputs with the gate's n (:417-441), which is only well defined for equal
+// n; equal shapes are required here.
 inline void gemv_q4_pair(const Q4Matrix &wg, const Q4Matrix &wu, const std::vector<float> &x,
                          std::vector<float> &out_gate, std::vector<float> &out_up) {
   require(wg.k() == wu.k() && wg.n() == wu.n(), "gemv_q4_pair: equal shapes");
