@@ -130,7 +130,10 @@ int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks);
  * the GEMM (m >= 65, long rows at m >= 49, or k > 32768) builds the image
  * itself, which allocates -- so call this before capturing such a call in a
  * graph or passing the matrix to lgh_q4_gemm_dev_noalloc.  LGH_ERR_SHAPE if
- * the image would exceed 2 GiB.  No reference counterpart: llm-cpu's Q4Matrix
+ * the image would exceed 2 GiB (about 2.4e9 weights): such a matrix never
+ * has one, and the calls that would use it run the matrix-core batch kernel
+ * on its nibble planes instead, 64 tokens per launch, with the same results'
+ * tolerance.  No reference counterpart: llm-cpu's Q4Matrix
  * packs its tiles (and AMX panels) at load, gemv_q4.rs:116-209. */
 int lgh_q4_prepare_gemm(lgh_ctx *ctx, const lgh_q4 *w);
 /* Device bytes the matrix holds: the nibble and scale planes, plus the GEMM

@@ -680,6 +680,8 @@ static int check_mode(lgh_ctx *ctx, int mode) {
 
 static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
                           float *const *y_dev, size_t m, int mode);
+static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
+                       const int8_t *codes_dev, const float *scales_dev, float *const *y_dev, size_t m, int mode);
 
 static int launch_gemv(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *w0, float *y0, const lgh_q4 *w1, float *y1,
                        const float *x, int mode) {
@@ -744,6 +746,10 @@ int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, co
   if (!lgh::plan_q4_gemv(w->n, w->bpr, 1).ok) {
     // K > 32768: the codes and scales become the GEMM's activation image (one token), and the
     // GEMM folds every block as the GEMV does.
+    if (!mx_fits(w)) {
+      float *ys[1] = {y_dev};
+      return mma_chunked(ctx, grow_ws(ctx), &w, 1, nullptr, qs_dev, scales_dev, ys, 1, mode);
+    }
     if (int r = ensure_mx(ctx, w)) return r;
     const lgh_q4 *ws1[1] = {w};
     const int splits = lgh::plan_q4_gemm_splits(ws1, 1, 1);
@@ -809,6 +815,52 @@ int lgh_act_quant_dev(lgh_ctx *ctx, const float *x_dev, size_t m, size_t k, int8
   return LGH_OK;
 }
 
+// Matrices whose GEMM image would not fit 31-bit buffer offsets (over 2 GiB,
+// ~2.4e9 weights) have none.  Their calls that would take the GEMM (m >= 65,
+// long rows at m >= 49, m == 1 with k > 32768) run the matrix-core batch
+// kernel on the nibble planes instead, up to 64 tokens per launch.  With
+// codes_dev / scales_dev (ActQ8 codes and block scales of the m rows) the
+// image is built from them instead of from x.
+static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
+                       const int8_t *codes_dev, const float *scales_dev, float *const *y_dev, size_t m, int mode) {
+  const size_t k = w[0]->k, bpr = w[0]->bpr, pq = (bpr + 3) / 4;
+  struct Layout {
+    size_t o_ci, o_si, o_rs, bytes;
+  };
+  auto layout = [&](size_t c) {
+    const size_t mt = (c + 15) / 16;
+    Layout l{};
+    Carve cv;
+    l.o_ci = cv.take(mt * pq * 2 * 1024);
+    l.o_si = cv.take(mt * pq * 256);
+    l.o_rs = cv.take(c * sizeof(float));
+    l.bytes = cv.off;
+    return l;
+  };
+  size_t chunk = std::min<size_t>(m, 64);
+  Layout lay = layout(chunk);
+  while (lay.bytes > wsp.limit() && chunk > 16) {
+    chunk = std::max<size_t>(16, chunk / 2 / 16 * 16);
+    lay = layout(chunk);
+  }
+  char *ws = nullptr;
+  if (int r = wsp.get(lay.bytes, &ws)) return r;
+  auto *ci = reinterpret_cast<uint8_t *>(ws + lay.o_ci);
+  auto *si = reinterpret_cast<float *>(ws + lay.o_si);
+  for (size_t m0 = 0; m0 < m; m0 += chunk) {
+    const size_t mc = std::min(chunk, m - m0);
+    if (codes_dev)
+      LGH_HIP(ctx, lgh::launch_act_codes_mma(codes_dev + m0 * k, scales_dev + m0 * bpr, mc, k, ci, si, ctx->stream));
+    else
+      LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev + m0 * k, mc, k, ctx->act_mode, ci, si,
+                                             reinterpret_cast<float *>(ws + lay.o_rs), ctx->stream));
+    for (int j = 0; j < nmat; j++)
+      if (w[j]->n)
+        LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w[j], ci, si, y_dev[j] + m0 * w[j]->n, mc, mode, ctx->stream, true));
+  }
+  return LGH_OK;
+}
+
 // y[j] = x @ W[j]^T for 1..3 matrices with the same k, m rows of x: the
 // activation quantization of each route (the MMA image, the GEMM's operand
 // image) is done once and read by every matrix.  m == 1 and m <= 4 quantize
@@ -862,6 +914,8 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
       if (w[j]->n) LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w[j], ci, si, y_dev[j], m, mode, ctx->stream));
     return LGH_OK;
   }
+  for (int j = 0; j < nmat; j++)
+    if (w[j]->n && !mx_fits(w[j])) return mma_chunked(ctx, wsp, w, nmat, x_dev, nullptr, nullptr, y_dev, m, mode);
   for (int j = 0; j < nmat; j++) {
     if (!w[j]->n) continue;
     if (wsp.fixed) {  // building the image allocates

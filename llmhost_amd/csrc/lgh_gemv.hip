@@ -881,13 +881,14 @@ int gemv_plans_uncovered() {
       }
   // The ragged MMA planner: every token count it takes, row lengths 1..1024
   // blocks, row counts on both sides of its 8192-row and 16384-row tests.
-  for (size_t m = 1; m <= 65; m++)
-    for (size_t bpr = 1; bpr <= 1024; bpr++)
-      for (size_t n : {size_t{1}, size_t{16}, size_t{8191}, size_t{8192}, size_t{8193}, size_t{16383},
-                       size_t{16384}, size_t{16385}, size_t{1} << 20}) {
-        const Q4MmaPlan p = plan_q4_mma(n, m, bpr);
-        if (p.ok && !mma_shape_compiled(p.TT, p.KW, p.CB, p.RG)) missing++;
-      }
+  for (int any = 0; any < 2; any++)
+    for (size_t m = 1; m <= 65; m++)
+      for (size_t bpr = 1; bpr <= 1024; bpr++)
+        for (size_t n : {size_t{1}, size_t{16}, size_t{8191}, size_t{8192}, size_t{8193}, size_t{16383},
+                         size_t{16384}, size_t{16385}, size_t{1} << 20}) {
+          const Q4MmaPlan p = plan_q4_mma(n, m, bpr, any != 0);
+          if (p.ok && !mma_shape_compiled(p.TT, p.KW, p.CB, p.RG)) missing++;
+        }
   return missing;
 }
 
@@ -1024,14 +1025,14 @@ hipError_t launch_q4_gemv_batch(const lgh_q4 *w, const float *x, const int8_t *c
 // tiles, two for three or four (measured at N=8192, K=2048: more, smaller waves are
 // faster while a chunk's registers stay small, then occupancy wins); RG row
 // groups make the workgroup at least 4 waves.
-Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr) {
+Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr, bool any_shape) {
   Q4MmaPlan p{};
-  if (m < 2 || m > 64 || bpr == 0 || n == 0) return p;
+  if (m < (any_shape ? 1u : 2u) || m > 64 || bpr == 0 || n == 0) return p;
   // Four token tiles over long rows: the fp6 GEMM is faster (M=64, whole
   // call: K=8192, N=1536 / 2048 / 8192 20.4 / 20.7 / 36.6 -> 18.5 / 19.3 /
   // 29.8 us; K=4096, N=16384 39.1 -> 30.9 us), but not where its grid is
   // small (K=4096, N=4096: 13.7 us here, 18.0 us on the GEMM).
-  if (m > 48 && (bpr >= 256 || (bpr >= 128 && n >= 16384))) return p;
+  if (!any_shape && m > 48 && (bpr >= 256 || (bpr >= 128 && n >= 16384))) return p;
   p.TT = static_cast<int>((m + 15) / 16);
   p.CB = 8;
   // Three token tiles over rows of >= 48 blocks and up to 8192 rows: 4-block
@@ -1052,8 +1053,8 @@ Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr) {
 }
 
 hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
-                              int mode, hipStream_t st) {
-  const Q4MmaPlan p = plan_q4_mma(w->n, m, w->bpr);
+                              int mode, hipStream_t st, bool any_shape) {
+  const Q4MmaPlan p = plan_q4_mma(w->n, m, w->bpr, any_shape);
   if (!p.ok) return hipErrorInvalidValue;
   Q4MmaArgs a{w->qs, w->sc, codes, scales, y, static_cast<int>(w->n), static_cast<int>(w->bpr), static_cast<int>(m),
               mode, static_cast<int>((m + 15) / 16), static_cast<int>((w->bpr + 3) / 4)};

@@ -184,11 +184,16 @@ struct Q4MmaPlan {
   int TT, KW, CB, RG;
   bool ok;
 };
-Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr);
+// any_shape: a plan for every 1 <= m <= 64 and row length, also where the
+// route table prefers the GEMM (for matrices that cannot hold a GEMM image).
+Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr, bool any_shape = false);
 hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row, uint8_t *codes, float *scales,
                                 float *row_scale, hipStream_t stream);
+// The same image from ActQ8 codes [m][k] and block scales [m][k/32].
+hipError_t launch_act_codes_mma(const int8_t *aq, const float *as, size_t m, size_t k, uint8_t *codes,
+                                float *scales, hipStream_t stream);
 hipError_t launch_q4_gemv_mma(const lgh_q4 *w, const uint8_t *codes, const float *scales, float *y, size_t m,
-                              int mode, hipStream_t stream);
+                              int mode, hipStream_t stream, bool any_shape = false);
 // Q8_0 GEMV; K ranges of kQ8GemvMaxK (the Q4 GEMV plan's reach) and 65535
 // tokens per launch.  With norm_w not null (k <= kQ8GemvMaxK only) each
 // token's row is rms_norm'd in the prologue (eps as rms_norm).

@@ -365,6 +365,25 @@ __global__ __launch_bounds__(kThreads) void act_quant_mma_kernel(const float *__
   if (g8 == 0) scales[((static_cast<size_t>(t >> 4) * pq + (b >> 2)) * 16 + (t & 15)) * 4 + (b & 3)] = ok ? scale : 0.0f;
 }
 
+// The same image from ActQ8 codes and block scales already computed (the
+// prepared-activation GEMV of a matrix without a GEMM image).
+__global__ __launch_bounds__(kThreads) void act_codes_mma_kernel(const int8_t *__restrict__ aq,
+                                                                 const float *__restrict__ as, int m, int bpr,
+                                                                 int pq, size_t groups, uint8_t *codes,
+                                                                 float *scales) {
+  const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
+  if (gi >= groups) return;
+  const int g8 = threadIdx.x & 7;
+  const int t = static_cast<int>(gi / (4 * pq)), b = static_cast<int>(gi % (4 * pq));
+  const bool ok = t < m && b < bpr;
+  const size_t blk = static_cast<size_t>(t) * bpr + b;
+  const int q = ok ? reinterpret_cast<const int *>(aq)[blk * 8 + g8] : 0;
+  const size_t pair = static_cast<size_t>(t >> 4) * (2 * pq) + (b >> 1);
+  const int lane = (t & 15) + 16 * (g8 >> 1);
+  *reinterpret_cast<int *>(codes + (pair * 64 + lane) * 16 + (b & 1) * 8 + (g8 & 1) * 4) = q;
+  if (g8 == 0) scales[((static_cast<size_t>(t >> 4) * pq + (b >> 2)) * 16 + (t & 15)) * 4 + (b & 3)] = ok ? as[blk] : 0.0f;
+}
+
 inline unsigned blocks_for(size_t items, unsigned per) {
   return static_cast<unsigned>((items + per - 1) / per);
 }
@@ -412,6 +431,16 @@ hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row,
   hipLaunchKernelGGL(act_quant_mma_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x,
                      static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pq), per_row, row_scale, groups,
                      codes, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_codes_mma(const int8_t *aq, const float *as, size_t m, size_t k, uint8_t *codes,
+                                float *scales, hipStream_t st) {
+  const size_t bpr = k / 32, pq = (bpr + 3) / 4, mt = (m + 15) / 16;
+  if (m == 0 || bpr == 0) return hipSuccess;
+  const size_t groups = mt * 16 * pq * 4;
+  hipLaunchKernelGGL(act_codes_mma_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, aq, as,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pq), groups, codes, scales);
   return hipGetLastError();
 }
 

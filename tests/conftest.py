@@ -102,6 +102,23 @@ def q8_exact_terms(blocks, n, k, qs, sa):
     return terms.sum(axis=-1), np.sqrt((terms * terms).sum(axis=-1))
 
 
+def q4_exact_terms(blocks, n, k, qs, sa):
+    """As q8_exact_terms for BlockQ4 [n, k/32]: element 2j of a block is the low nibble of qs[j],
+    element 2j+1 the high one, each a signed 4-bit code (crates/llm-quant/src/lib.rs:83-92)."""
+    nb = k // 32
+    raw = blocks.reshape(n, nb)["qs"].astype(np.int64)                        # [n, nb, 16]
+    w = np.empty((n, nb, 32), np.int64)
+    w[..., 0::2] = raw & 15
+    w[..., 1::2] = raw >> 4
+    w[w >= 8] -= 16
+    sw = blocks.reshape(n, nb)["scale"].view(np.float16).astype(np.float64)
+    q = np.asarray(qs, np.int64).reshape(-1, nb, 32)
+    s = np.asarray(sa, np.float64).reshape(-1, nb)
+    dots = np.einsum("nbj,tbj->tnb", w, q)
+    terms = dots.astype(np.float64) * sw[None] * s[:, None, :]
+    return terms.sum(axis=-1), np.sqrt((terms * terms).sum(axis=-1))
+
+
 def summation_allowance(R, nterms):
     """What the order of an f32 summation of nterms terms can move the result by, at the scale R of
     its partial sums: 8 u sqrt(n) R with u = 2^-24 (the probabilistic rounding-error bound's form;
