@@ -429,6 +429,45 @@ struct ReduceMulti {
   int splits, mode;
 };
 
+// Four outputs per thread, when every matrix's m * n is a multiple of 4 and
+// every y is 16-byte aligned (partials always are): no float4 straddles two
+// matrices.  The same additions in the same order as the scalar kernel
+// (M=512, K=8192, N=1536: 35.3 -> 33.6 us; M=65, K=8192, N=8192: 34.6 ->
+// 33.1 us; M=130, K=8192, N=8192: 46.8 -> 44.5 us; interleaved A/B).
+__global__ __launch_bounds__(256) void splitk_reduce_multi4_kernel(ReduceMulti r) {
+  const size_t i = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= r.end[2]) return;
+  int j = 0;
+  size_t begin = 0;
+  if (i >= r.end[0]) {
+    j = 1;
+    begin = r.end[0];
+    if (i >= r.end[1]) {
+      j = 2;
+      begin = r.end[1];
+    }
+  }
+  const size_t total = r.end[j] - begin, e = i - begin;
+  const float *part = r.part[j];
+  float4 v = *reinterpret_cast<const float4 *>(part + e);
+  for (int z = 1; z < r.splits; z++) {
+    const float4 p = *reinterpret_cast<const float4 *>(part + static_cast<size_t>(z) * total + e);
+    v.x += p.x;
+    v.y += p.y;
+    v.z += p.z;
+    v.w += p.w;
+  }
+  float4 *y = reinterpret_cast<float4 *>(r.y[j] + e);
+  if (r.mode != LGH_ASSIGN) {
+    const float4 o = *y;
+    v.x = apply_mode(o.x, v.x, r.mode);
+    v.y = apply_mode(o.y, v.y, r.mode);
+    v.z = apply_mode(o.z, v.z, r.mode);
+    v.w = apply_mode(o.w, v.w, r.mode);
+  }
+  *y = v;
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce_multi_kernel(ReduceMulti r) {
   size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= r.end[2]) return;
@@ -492,8 +531,16 @@ hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
   }
   r.splits = splits;
   r.mode = gm.g[0].mode;
-  hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3(static_cast<unsigned>((end + 255) / 256)), dim3(256), 0, st,
-                     r);
+  bool vec = true;
+  for (int j = 0; j < nmat; j++)
+    vec = vec && (static_cast<size_t>(gm.g[j].m) * gm.g[j].n) % 4 == 0 &&
+          (reinterpret_cast<uintptr_t>(gm.g[j].y) & 15u) == 0;
+  if (vec)
+    hipLaunchKernelGGL(splitk_reduce_multi4_kernel, dim3(static_cast<unsigned>((end / 4 + 255) / 256)), dim3(256), 0,
+                       st, r);
+  else
+    hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3(static_cast<unsigned>((end + 255) / 256)), dim3(256), 0, st,
+                       r);
   return hipGetLastError();
 }
 

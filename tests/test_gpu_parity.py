@@ -9,7 +9,7 @@ and its VNNI kernel (the production CPU path) on identical seeded inputs.
 import numpy as np
 import pytest
 
-from llmhost_amd import formats, q4, synth
+from llmhost_amd import _ffi, formats, q4, synth
 from llmhost_amd.formats import BLOCK_Q4
 
 from .conftest import assert_close, assert_close_with_flips, q8_exact_terms, summation_allowance
@@ -572,6 +572,39 @@ def test_split_k_gemv_is_deterministic(gpu_ctx, oracle):
         outs.append(y)
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
     assert_close(outs[0], oracle.gemv_q4(oracle.Q4Matrix(n, k, blocks), x, threads=8), what="split-K")
+
+
+@pytest.mark.parametrize("mode", [_ffi.LGH_ASSIGN, _ffi.LGH_ADD_F64, _ffi.LGH_ADD_F32])
+def test_split_k_reduce_vector_and_scalar_forms(gpu_ctx, oracle, mode):
+    """The split-K reduce adds four outputs per thread when every m * n is a multiple of 4 and y
+    is 16-byte aligned, else one: N=1536 (vector), N=1531 (odd: scalar) and N=1536 into a y one
+    float past an aligned address (scalar), against the oracle and bit-equal between the forms."""
+    import torch
+
+    m, k = 65, 8192  # 65 tokens x 8192: three 32-token tiles, K split
+    results = {}
+    for n in (1536, 1531):
+        blocks = synth.q4_blocks(70 + n, n, k)
+        w = q4.Q4Matrix.from_blocks(n, k, blocks, gpu_ctx)
+        x = synth.activations(71, m, k)
+        y0 = synth.activations(72 + n, m, n)
+        xd = torch.from_numpy(x).cuda()
+        buf = torch.zeros(m * n + 4, device="cuda")
+        for off in (0, 1) if n == 1536 else (0,):
+            y = buf[off:off + m * n].view(m, n)
+            y.copy_(torch.from_numpy(y0))
+            {_ffi.LGH_ASSIGN: q4.gemm_q4, _ffi.LGH_ADD_F64: q4.gemm_q4_add,
+             _ffi.LGH_ADD_F32: q4.apply_add_inplace}[mode](w, xd, y, m)
+            torch.cuda.synchronize()
+            results[(n, off)] = y.cpu().numpy()
+        ref = oracle.gemm_q4(oracle.Q4Matrix(n, k, blocks), x, m, threads=8)
+        if mode == _ffi.LGH_ASSIGN:
+            assert_close(results[(n, 0)], ref, what=f"n={n}")
+        else:
+            got = results[(n, 0)].astype(np.float64) - y0.astype(np.float64)
+            assert_close(got, ref, atol=2e-4, what=f"n={n} mode={mode}")
+        w.free()
+    assert np.array_equal(results[(1536, 0)], results[(1536, 1)])
 
 
 def test_graph_replay_matches_eager(gpu_ctx):
