@@ -478,7 +478,8 @@ int lgh_q4_from_f32(lgh_ctx *ctx, const float *wf, size_t n, size_t k, lgh_q4 **
 
 int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w || !blocks) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = check_mat(ctx, w)) return r;
+  if (!blocks) return fail(ctx, LGH_ERR_INVALID_ARG, "null destination");
   if (int r = set_device(ctx)) return r;
   const size_t nb = w->n * w->bpr, bytes = nb * LGH_BLOCK_Q4_BYTES;
   if (!bytes) return LGH_OK;
@@ -656,7 +657,8 @@ int lgh_q8_from_f32(lgh_ctx *ctx, const float *wf, size_t n, size_t k, lgh_q8 **
 
 int lgh_q8_download(lgh_ctx *ctx, const lgh_q8 *w, void *blocks) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
-  if (!w || !blocks) return fail(ctx, LGH_ERR_INVALID_ARG, "null argument");
+  if (int r = check_mat(ctx, w)) return r;
+  if (!blocks) return fail(ctx, LGH_ERR_INVALID_ARG, "null destination");
   if (int r = set_device(ctx)) return r;
   const size_t nb = w->n * w->bpr, bytes = nb * LGH_BLOCK_Q8_BYTES;
   if (!bytes) return LGH_OK;
