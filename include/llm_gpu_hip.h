@@ -219,7 +219,9 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
  * process ends; the call allocates, frees and synchronizes nothing.  Token
  * chunks shrink until their scratch fits; a call whose 32-token chunk still
  * needs more returns LGH_ERR_SHAPE.  Routes that need the matrix's GEMM image
- * return LGH_ERR_INVALID_ARG unless lgh_q4_prepare_gemm has built it.  Every
+ * return LGH_ERR_INVALID_ARG unless lgh_q4_prepare_gemm has built it (a
+ * matrix too large for one needs none: its chunks of <= 64 tokens, 16 when
+ * the row is too long for 64, run on the nibble planes).  Every
  * context on a GPU shares that GPU's array and it keeps the last call's
  * contents: calls that overlap on one GPU (several contexts or streams)
  * race, so the caller serializes them.  Results equal lgh_q4_gemm_dev's. */
