@@ -73,6 +73,11 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_gate_up_kernel(FfnUpArgs a) {
     xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * kFfnThreads) * 16u);
     nv[j] = buf_load_f4(nr, static_cast<uint32_t>(tid + j * kFfnThreads) * 16u);
   }
+  // (1b) The norm and the quantization wait for every wave's hidden: queue
+  // those requests before any wave's weight requests.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
   // (2) every weight load of this lane: its row of W1 and of W3, BPL blocks each.
   const size_t blk0 = static_cast<size_t>(row0) * bpr;

@@ -163,13 +163,15 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     }
   }
 
-  // (1b) x at least twice the workgroup's float4s, or (PREQ) the codes: every
-  // wave's activation requests are queued before any wave's weight requests.
-  // Without the barrier, waves that start later issue them behind the earlier
-  // waves' weight loads: at K = 8192 x arrived up to 1.7 us after issue (0.8
-  // us with it), and the codes GEMV of the FFN block's down projection took
-  // 3.98 us against 3.78 us with it (interleaved A/B).
-  if constexpr (PREQ || PAIRS) {
+  // (1b) x at least twice the workgroup's float4s, (PREQ) the codes, or (NORM)
+  // x and the norm weight: every wave's activation requests are queued before
+  // any wave's weight requests.  Without the barrier, waves that start later
+  // issue them behind the earlier waves' weight loads: at K = 8192 x arrived
+  // up to 1.7 us after issue (0.8 us with it); the codes GEMV of the FFN
+  // block's down projection took 3.98 us against 3.78 us with it, the norm +
+  // conv in_proj (K=1536, N=4608) 4.0 against 3.5 us and the norm + gate/up
+  // pair 5.1 against 4.76 us (interleaved A/B).
+  if constexpr (PREQ || PAIRS || NORM) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -737,6 +739,8 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
       xv[j] = buf_load_f4(xr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
       if constexpr (NORM) nv[j] = buf_load_f4(nr, static_cast<uint32_t>(tid + j * THREADS) * 16u);
     }
+    // No x-before-weights barrier with NORM here: the tied head (K=1536,
+    // N=65536, 16-wave workgroups) measured 19.7 -> 20.2 us with one.
   }
 
   // (2) every weight load of this lane (rows past n fall outside the resource).
