@@ -325,6 +325,16 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_batch_kernel(Q4BatchArgs a)
     }
   }
 
+  // (1b) PREQ over four or more K slices: every wave's code requests before
+  // any wave's weight requests (M=2 / 4, K=8192, N=2048: 7.41 / 7.49 ->
+  // 7.26 / 7.32 us; the x path at K=2048 and the codes at K=4096 measured
+  // no gain or a loss, interleaved A/B).
+  if constexpr (PREQ && KW >= 4) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
   // (2) every weight load of this lane (rows past n read as 0).
   const size_t blk0 = static_cast<size_t>(row0) * bpr;
   const auto wr = make_rsrc(a.qs + blk0 * 16, static_cast<uint32_t>(rows * bpr) * 16u);
