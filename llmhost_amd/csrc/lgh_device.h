@@ -465,6 +465,12 @@ __device__ __forceinline__ void store_row(float *y, int row, float acc16, int mo
   y[row] = mode == LGH_ASSIGN ? v : apply_mode(y[row], v, mode);
 }
 
+// store_row with the old y[row] read earlier by the same lane.
+__device__ __forceinline__ void store_row_old(float *y, int row, float acc16, int mode, float y_old) {
+  const float v = acc16 * 0.0625f;
+  y[row] = mode == LGH_ASSIGN ? v : apply_mode(y_old, v, mode);
+}
+
 // ---- MX-fp6 operand codes ----------------------------------------------------
 // The GEMM feeds integer operands to the fp6 matrix cores as OCP MX FP6 E3M2
 // codes (1 sign, 3 exponent bits with bias 3, 2 mantissa bits).  Every

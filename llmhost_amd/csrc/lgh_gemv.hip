@@ -225,13 +225,25 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
     const int d = dot_q4_block16(w[j], ap[0], ap[1]);
     acc = fmaf(static_cast<float>(d), h2f(s[j]) * s_sa[kbc], acc);
   }
+  // (4b) AddF64 / AddF32: the old y of the row this lane stores, read now so
+  // that its round trip overlaps the reductions (branch-free: the other lanes
+  // read past the range).  Read after the reductions it cost 0.35 us over
+  // Assign; here 0.1-0.25 us (K=8192, N=1536 AddF64 3.88 -> 3.65 us; K=1536,
+  // N=8192 3.36 -> 3.24 us; interleaved A/B).  Read in the prologue instead,
+  // beside the weight loads, it was slower than either (3.79 -> 4.30 us).
+  float y_old = 0.0f;
+  if (a.mode != LGH_ASSIGN) {  // uniform
+    const int srow = KW == 1 ? (c == 0 && r < rows ? row0 + r : -1) : (ks == 0 && lane < rows ? row0 + lane : -1);
+    y_old = buf_load_f32(make_rsrc(y, static_cast<uint32_t>(n) * 4u),
+                         srow >= 0 ? static_cast<uint32_t>(srow) * 4u : kOOB);
+  }
   // (5) 16-lane row sums (every lane of a DPP row ends with its row's sum).
   acc += dpp<0xB1>(acc);   // quad_perm [1,0,3,2]
   acc += dpp<0x4E>(acc);   // quad_perm [2,3,0,1]
   acc += dpp<0x141>(acc);  // row_half_mirror
   acc += dpp<0x140>(acc);  // row_mirror
   if constexpr (KW == 1) {
-    if (c == 0 && r < rows) store_row(y, row0 + r, acc, a.mode);
+    if (c == 0 && r < rows) store_row_old(y, row0 + r, acc, a.mode, y_old);
   } else {
     if (c == 0) s_part[(rg * 4 + r) * KW + ks] = acc;
     __syncthreads();
@@ -239,7 +251,7 @@ __global__ __launch_bounds__(W * kWave) void q4_gemv_kernel(Q4GemvArgs a) {
       float sum = 0.0f;
 #pragma unroll
       for (int k = 0; k < KW; k++) sum += s_part[(rg * 4 + lane) * KW + k];
-      store_row(y, row0 + lane, sum, a.mode);
+      store_row_old(y, row0 + lane, sum, a.mode, y_old);
     }
   }
 }
