@@ -711,7 +711,16 @@ struct Q8GemvArgs {
 // always quantized per block (weights.rs:197); token blockIdx.y.  NORM: each
 // token's row is rms_norm'd in the prologue first, as q4_gemv_kernel does (the
 // final norm before the output head, crates/llm-engine/src/lfm2.rs:559-567).
-template <int BPL, int KW, int W, bool NORM = false>
+// HALF: lane c of a DPP row loads half c & 1 of block (c >> 1) + 8 j (16 B
+// each), so a row's 16 lanes read 256 contiguous bytes per instruction; the
+// two halves' integer dots meet by one DPP add, and the even lane folds the
+// block.  Without it lane c loads both halves of block c + 16 j, and each
+// instruction reads every other 16 bytes of 512.  Measured (interleaved A/B):
+// the tied head K=1536, N=65536 19.3 -> 17.6 us; K=8192, N=1536 4.88 ->
+// 4.31 us; K=4096, N=16384 14.6 -> 13.2 us; but K=N=1536 2.52 -> 2.63 us and
+// K=1536, N=2048 2.65 -> 2.76 us, so small matrices keep the whole-block
+// lanes.
+template <int BPL, int KW, int W, bool NORM = false, bool HALF = false>
 __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   constexpr int THREADS = W * kWave;
   constexpr int KB = 16 * BPL * KW;
@@ -771,15 +780,24 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   const uint32_t span = rows > 0 ? static_cast<uint32_t>((rows - 1) * stride + bpr) : 0u;
   const auto wr = make_rsrc(a.qs + blk0 * 32, span * 32u);
   const auto sr = make_rsrc(a.sc + blk0, span * 2u);
-  uint4 w0[BPL], w1[BPL];
-  uint16_t s[BPL];
+  constexpr int NL = HALF ? 2 * BPL : BPL;  // loads of 16 B per lane (x2 without HALF)
+  const int hb = ks * 16 * BPL + (c >> 1), half = c & 1;
+  uint4 w0[NL], w1[HALF ? 1 : BPL];
+  uint16_t s[NL];
 #pragma unroll
-  for (int j = 0; j < BPL; j++) {
-    const int kb = kb0 + 16 * j;
-    const uint32_t blk = static_cast<uint32_t>(r * stride + kb);
-    w0[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u : kOOB);
-    w1[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u : kOOB);
-    s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
+  for (int j = 0; j < NL; j++) {
+    if constexpr (HALF) {
+      const int kb = hb + 8 * j;
+      const uint32_t blk = static_cast<uint32_t>(r * stride + kb);
+      w0[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u * static_cast<uint32_t>(half) : kOOB);
+      s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
+    } else {
+      const int kb = kb0 + 16 * j;
+      const uint32_t blk = static_cast<uint32_t>(r * stride + kb);
+      w0[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u : kOOB);
+      w1[j] = buf_load16<kAuxNT>(wr, kb < bpr ? blk * 32u + 16u : kOOB);
+      s[j] = buf_load_u16(sr, kb < bpr ? blk * 2u : kOOB);
+    }
   }
 
   // (2b) NORM: x = nw * (x * scale).
@@ -795,12 +813,26 @@ __global__ __launch_bounds__(W * kWave) void q8_gemv_kernel(Q8GemvArgs a) {
   // and scale and reads block 0's codes, so its term is exactly 0.
   float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < BPL; j++) {
-    const int kb = kb0 + 16 * j;
-    const int kbc = kb < bpr ? kb : 0;
-    const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kbc * 32);
-    const int d = dot_q8_block(w0[j], w1[j], ap[0], ap[1]);
-    acc += (static_cast<float>(d) * h2f(s[j])) * s_sa[kbc];
+  for (int j = 0; j < NL; j++) {
+    if constexpr (HALF) {
+      const int kb = hb + 8 * j;
+      const int kbc = kb < bpr ? kb : 0;
+      const v4i ah = reinterpret_cast<const v4i *>(s_qs + kbc * 32)[half];
+      int d = 0;
+      d = sdot4(static_cast<int>(w0[j].x), ah.x, d);
+      d = sdot4(static_cast<int>(w0[j].y), ah.y, d);
+      d = sdot4(static_cast<int>(w0[j].z), ah.z, d);
+      d = sdot4(static_cast<int>(w0[j].w), ah.w, d);
+      d += __builtin_amdgcn_update_dpp(0, d, 0xB1, 0xf, 0xf, false);  // + the other half (lane c ^ 1)
+      const float t = (static_cast<float>(d) * h2f(s[j])) * s_sa[kbc];
+      acc += half ? 0.0f : t;
+    } else {
+      const int kb = kb0 + 16 * j;
+      const int kbc = kb < bpr ? kb : 0;
+      const v4i *ap = reinterpret_cast<const v4i *>(s_qs + kbc * 32);
+      const int d = dot_q8_block(w0[j], w1[j], ap[0], ap[1]);
+      acc += (static_cast<float>(d) * h2f(s[j])) * s_sa[kbc];
+    }
   }
   // (5) 16-lane row sums, slices in order, store.
   acc += dpp<0xB1>(acc);
@@ -1128,12 +1160,18 @@ hipError_t launch_q8_range(const lgh_q8 *w, const float *x, float *y, size_t tok
                add ? 1 : 0};
   const dim3 grid(static_cast<unsigned>(p.wgs_per_mat), static_cast<unsigned>(tokens));
   const bool norm = norm_w != nullptr;
+  const bool half = w->n * nb >= (size_t{1} << 17);  // >= 4.5 MB of blocks: contiguous half-block loads
 #define LGH_Q8(BB, KK, WW)                                                                            \
   if (p.BPL == BB && p.KW == KK && p.W == WW) {                                                       \
-    if (norm)                                                                                         \
-      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, true>), grid, dim3(WW * kWave), 0, st, a);       \
+    const dim3 blk(WW * kWave);                                                                       \
+    if (norm && half)                                                                                 \
+      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, true, true>), grid, blk, 0, st, a);              \
+    else if (norm)                                                                                    \
+      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, true, false>), grid, blk, 0, st, a);             \
+    else if (half)                                                                                    \
+      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, false, true>), grid, blk, 0, st, a);             \
     else                                                                                              \
-      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, false>), grid, dim3(WW * kWave), 0, st, a);      \
+      hipLaunchKernelGGL((q8_gemv_kernel<BB, KK, WW, false, false>), grid, blk, 0, st, a);            \
     return hipGetLastError();                                                                         \
   }
   LGH_GEMV_SHAPES(LGH_Q8)
