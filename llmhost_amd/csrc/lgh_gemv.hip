@@ -1153,14 +1153,19 @@ hipError_t launch_q8_gemv(const lgh_q8 *w, const float *x, float *y, size_t toke
 // One launch of the Q8_0 GEMV over blocks [b0, b0 + nb) of every row.
 hipError_t launch_q8_range(const lgh_q8 *w, const float *x, float *y, size_t tokens, const float *norm_w, float eps,
                            size_t b0, size_t nb, bool add, hipStream_t st) {
-  const Q4GemvPlan p = plan_q4_gemv(w->n, nb, 1, false);
+  // Matrices of >= 2^17 blocks load contiguous half blocks (HALF); with the
+  // norm prologue they also take the 8-wave plan (`narrow`): every workgroup
+  // norms and quantizes x before its first dot, and with 16-wave workgroups
+  // the tied head runs 4 rounds of them, one at a time per CU (norm + head
+  // 20.7 -> 17.6 us; the head alone keeps 16 waves: 17.6 against 18.0 us).
+  const bool half = w->n * nb >= (size_t{1} << 17);
+  const bool norm = norm_w != nullptr;
+  const Q4GemvPlan p = plan_q4_gemv(w->n, nb, 1, norm && half);
   if (!p.ok || tokens > 65535) return hipErrorInvalidValue;
   Q8GemvArgs a{w->qs, w->sc, x, y, norm_w, 1.0 / static_cast<double>(w->k), eps, static_cast<int>(w->n),
                static_cast<int>(nb), static_cast<int>(w->bpr), static_cast<int>(b0), static_cast<int>(w->k),
                add ? 1 : 0};
   const dim3 grid(static_cast<unsigned>(p.wgs_per_mat), static_cast<unsigned>(tokens));
-  const bool norm = norm_w != nullptr;
-  const bool half = w->n * nb >= (size_t{1} << 17);  // >= 4.5 MB of blocks: contiguous half-block loads
 #define LGH_Q8(BB, KK, WW)                                                                            \
   if (p.BPL == BB && p.KW == KK && p.W == WW) {                                                       \
     const dim3 blk(WW * kWave);                                                                       \
