@@ -177,10 +177,12 @@ def test_seam_mirror_block_sides(gpu_ctx, oracle):
 
 
 @pytest.mark.parametrize("tokens", [1, 2])
-@pytest.mark.parametrize("n,k", [(4096, 1536), (96, 64), (130, 2048), (64, 8192)])
+@pytest.mark.parametrize("n,k", [(4096, 1536), (96, 64), (130, 2048), (64, 8192), (65536, 1536)])
 def test_q8_head_with_final_norm(gpu_ctx, oracle, n, k, tokens):
     """rms_norm + the Q8_0 head in one launch: bit-identical to lgh_rms_norm then lgh_q8_gemv, and
-    within tolerance of the oracle's rms_norm then q8_apply (lfm2.rs:559-567)."""
+    within tolerance of the oracle's rms_norm then q8_apply (lfm2.rs:559-567).  Both matrix-size
+    regimes of the kernel (whole-block lanes; half-block lanes with 8-wave workgroups for the norm),
+    up to the tied head's shape."""
     from llmhost_amd import weights
 
     b8 = synth.q8_blocks(960 + n, n, k)
