@@ -4,7 +4,9 @@ same reference ops (crates/llm-engine/src/lfm2.rs:519-573, 784-911).
 Per layer: rms_norm + q / k / v (lgh_q4_norm_gemv, one launch), the output projection added onto
 hidden in f32 (LGH_ADD_F32; its input stands in for the attention output: the layer's q), the
 fused FFN block (lgh_q4_ffn_residual); then the final rms_norm + Q8_0 head (lgh_q8_norm_gemv).
-Every call reads, on the device, what the previous call wrote.
+Every call reads, on the device, what the previous call wrote.  Two layers, and the 16 of the
+benchmark's chained step (hidden 1536, ffn 8192, q/k/v 1536/256/256 rows, vocab 65536), with
+distinct weights per layer.
 
 Gate: each call, re-anchored on the device's own input to it, matches the oracle's op within the
 output tolerance (the FFN block with the allowance for the h codes an ulp of exp can flip, and the
@@ -22,21 +24,22 @@ from .conftest import ATOL, RTOL, assert_close, assert_close_with_flips, code_fl
 
 pytestmark = pytest.mark.gpu
 
-DIM, INTER, KV, VOCAB, LAYERS = 1536, 8192, 256, 65536, 2
+DIM, INTER, KV, VOCAB = 1536, 8192, 256, 65536
 
 
 def _ulp(a):
     return np.spacing(np.abs(np.asarray(a, np.float32))).astype(np.float64)
 
 
-def test_chained_decode_step(gpu_ctx, oracle):
+@pytest.mark.parametrize("n_layers", [2, 16])
+def test_chained_decode_step(gpu_ctx, oracle, n_layers):
     import torch
 
     rng_seed = 900
     shapes = {"q": (DIM, DIM), "k": (KV, DIM), "v": (KV, DIM), "o": (DIM, DIM), "w1": (INTER, DIM),
               "w3": (INTER, DIM), "w2": (DIM, INTER)}
     layers = []
-    for li in range(LAYERS):
+    for li in range(n_layers):
         L = {}
         for j, (name, (n, k)) in enumerate(shapes.items()):
             b = synth.q4_blocks(rng_seed + 10 * li + j, n, k)
@@ -86,7 +89,7 @@ def test_chained_decode_step(gpu_ctx, oracle):
         bound, flips, _ = code_flip_bound(L["w2"][0], DIM, INTER, q_ref.ravel(), s_ref.ravel(), hq, hs)
         assert flips <= INTER // 500, f"layer {li}: {flips} h codes differ"
         assert_close_with_flips(st["out"], ref_out, bound, what=f"layer {li} ffn ({flips} flips)")
-        if li + 1 < LAYERS:
+        if li + 1 < n_layers:
             assert np.array_equal(trace[li + 1]["in"], st["out"])
     ref_logits = oracle.q8_apply(hb, VOCAB, DIM, oracle.rms_norm(trace[-1]["out"], nw_final, 1e-5), 1, threads=8)
     assert_close(logits, ref_logits, what="final norm + q8 head")
