@@ -242,82 +242,101 @@ __device__ __forceinline__ void store_hl_group8(uint8_t *rec, int s, int tok, ui
   }
 }
 
-// Activations: a workgroup builds kActJobs half-records, each the h and l
-// code tiles of one block for one 32-token tile (1536 contiguous bytes) plus
-// its 32 scales.  8-lane group i quantizes token 32 T + i of the block; the
-// tiles are assembled in LDS and written with 16-byte stores, so every line
-// of the image is written whole by one workgroup.  The h / l E3M2 codes of
-// each int8 code come from a 256-entry LDS table built per workgroup
-// (q + 128 -> code(h) | code(l) << 6), a lookup in place of ~25 VALU per code.
-// One half-record per workgroup: whole GEMM calls at M=512, K=2048 / 10752
-// took 41.3 / 50.4 us with two and 42.2 / 50.8 us with four, 40.9 / 49.8 us
-// with one (the kernel is bound by its DRAM round trip; more workgroups
-// keep more of them in flight).
-constexpr int kActJobs = 1;
+// The h / l E3M2 codes of every int8 code q, indexed by q + 128:
+// code(h) | code(l) << 6, read from this table into LDS by each workgroup
+// (a lookup in place of ~25 VALU per code).
+struct HlTable {
+  uint16_t v[256];
+};
+constexpr uint16_t e3m2_const(int v) {
+  int a = v < 0 ? -v : v, e = 0;
+  while ((2 << e) <= a) e++;
+  return static_cast<uint16_t>(a == 0 ? 0 : ((v < 0 ? 0x20 : 0) | ((e + 3) << 2) | (((a << 2) >> e) & 3)));
+}
+constexpr HlTable make_hl_table() {
+  HlTable t{};
+  for (int i = 0; i < 256; i++) {
+    const int q = i - 128, h = (q + 8) >> 4, l = q - 16 * h;  // split_h_l
+    t.v[i] = static_cast<uint16_t>(e3m2_const(h) | (e3m2_const(l) << 6));
+  }
+  return t;
+}
+__constant__ HlTable kHlTable = make_hl_table();
 
+// Activations -> the GEMM's operand image, one record (r = token tile * pp +
+// block pair: 32 tokens x 2 blocks) per workgroup.  The 64 four-lane groups
+// each quantize one (token, block): group G = tid / 4 takes token G % 32 of
+// the tile and block G / 32 of the pair, lane g = tid % 4 elements 8g..8g+7
+// (two float4s; act_quant_group4 shares the block's max, scale and
+// reciprocal among 8 elements per lane).  Lane g's 8 codes are bits [48g,
+// 48g + 48) of the block's 192-bit h and l streams.  The record is assembled
+// in LDS and written with 16-byte stores, so every line of the image is
+// written whole by one workgroup.  Against one half-record per workgroup
+// with 8-lane groups and the table computed per workgroup (same image, bit
+// for bit; kernel trace): M=512, K=10752 7.96 -> 7.44 us, M=2048, K=10752
+// 25.0 -> 19.7 us, M=512, K=2048 unchanged (5.2 us); whole GEMM calls
+// 1.3-3.8% faster (interleaved A/B).
 __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, int m, int bpr,
-                                                                int pp, int per_row,
-                                                                const float *row_scale, uint32_t units,
-                                                                uint8_t *mxa) {
+                                                                int pp, int per_row, const float *row_scale,
+                                                                uint32_t recs, uint8_t *mxa) {
   __shared__ uint16_t s_hl[256];
-  __shared__ __align__(16) uint8_t s_tile[kActJobs][2 * kMxTile];
-  __shared__ float s_scale[kActJobs][32];
-  static_assert(kThreads == 256, "one table entry per thread, 32 groups = 32 tokens");
-  {
-    int h, l;
-    split_h_l(static_cast<int>(threadIdx.x) - 128, h, l);
-    s_hl[threadIdx.x] = static_cast<uint16_t>(e3m2_code(h) | (e3m2_code(l) << 6));
+  __shared__ __align__(16) uint8_t s_rec[kMxARec];
+  static_assert(kThreads == 256, "one table entry per thread, 64 groups = 32 tokens x 2 blocks");
+  const int tid = threadIdx.x, g = tid & 3, grp = tid >> 2, i = grp & 31, s = grp >> 5;
+  const uint32_t r = blockIdx.x;
+  const int t = static_cast<int>(r / static_cast<uint32_t>(pp)) * 32 + i;
+  const int blk = 2 * static_cast<int>(r % static_cast<uint32_t>(pp)) + s;
+  const bool ok = r < recs && t < m && blk < bpr;
+  float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+  if (ok) {
+    const float4 *src = reinterpret_cast<const float4 *>(x) + (static_cast<size_t>(t) * bpr + blk) * 8 + 2 * g;
+    a = src[0];
+    b = src[1];
   }
-  const int i = threadIdx.x >> 3, g = threadIdx.x & 7, r = g & 3;
-  const uint32_t bp2 = 2u * static_cast<uint32_t>(pp);
-  float4 v[kActJobs];
-#pragma unroll
-  for (int j = 0; j < kActJobs; j++) {
-    const uint32_t u = blockIdx.x * kActJobs + j;  // half-record: token tile u / bp2, block u % bp2
-    const int t = static_cast<int>(u / bp2) * 32 + i, b = static_cast<int>(u % bp2);
-    v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (u < units && t < m && b < bpr)
-      v[j] = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g];
-  }
+  s_hl[tid] = kHlTable.v[tid];
   __syncthreads();  // the table
+  const bool pr = ok && per_row;
+  const float rs = pr ? row_scale[t] : 0.0f;
+  float scale;
+  const uint2 q = act_quant_group4(a, b, pr, rs, scale);
+  // The 48-bit h and l streams of the lane's 8 codes (code e at bit 6e).
+  uint32_t hlo = 0, hhi = 0, llo = 0, lhi = 0;
 #pragma unroll
-  for (int j = 0; j < kActJobs; j++) {
-    const uint32_t u = blockIdx.x * kActJobs + j;
-    const int t = static_cast<int>(u / bp2) * 32 + i, b = static_cast<int>(u % bp2);
-    const bool ok = u < units && t < m && b < bpr;
-    const bool pr = ok && per_row;
-    const float rs = pr ? row_scale[t] : 0.0f;
-    float scale;
-    int sum;
-    const int q = act_quant_group8(v[j], pr, rs, scale, sum);
-    uint32_t vh = 0, vl = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t hl = s_hl[(q >> (8 * e)) + 128 & 255];
-      vh |= (hl & 63u) << (6 * e);
-      vl |= (hl >> 6) << (6 * e);
+  for (int e = 0; e < 8; e++) {
+    const uint32_t byte = ((e < 4 ? q.x : q.y) >> (8 * (e & 3))) & 0xFFu;
+    const uint32_t hl = s_hl[byte ^ 0x80u];
+    const uint32_t ch = hl & 63u, cl = hl >> 6;
+    const int bit = 6 * e;
+    if (bit < 32) {
+      hlo |= ch << bit;
+      llo |= cl << bit;
     }
-    const uint32_t dh = pack24_group8(vh), dl = pack24_group8(vl);
-    if (r < 3) {
-      const uint32_t off = mx_dword_off(i, 3 * (g >> 2) + r);
-      *reinterpret_cast<uint32_t *>(&s_tile[j][off]) = dh;
-      *reinterpret_cast<uint32_t *>(&s_tile[j][kMxTile + off]) = dl;
+    if (bit + 6 > 32) {  // code 5 straddles the two words
+      hhi |= bit >= 32 ? ch << (bit - 32) : ch >> (32 - bit);
+      lhi |= bit >= 32 ? cl << (bit - 32) : cl >> (32 - bit);
     }
-    if (g == 0) s_scale[j][i] = ok ? scale : 0.0f;
   }
+  // Dwords of the block's operand row: lane 0 -> 0, 1; lane 1 -> 2; lane 2
+  // -> 3, 4; lane 3 -> 5 (quad_perm [1,2,3,3] fetches lane g + 1's low word).
+  const uint32_t nh = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hlo), 0xF9, 0xf, 0xf, false));
+  const uint32_t nl = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(llo), 0xF9, 0xf, 0xf, false));
+  uint8_t *th = s_rec + (2 * s) * kMxTile, *tl = th + kMxTile;
+  if ((g & 1) == 0) {
+    const int d = 3 * (g >> 1);
+    *reinterpret_cast<uint32_t *>(th + mx_dword_off(i, d)) = hlo;
+    *reinterpret_cast<uint32_t *>(tl + mx_dword_off(i, d)) = llo;
+    *reinterpret_cast<uint32_t *>(th + mx_dword_off(i, d + 1)) = hhi | (nh << 16);
+    *reinterpret_cast<uint32_t *>(tl + mx_dword_off(i, d + 1)) = lhi | (nl << 16);
+  } else {
+    const int d = 3 * (g >> 1) + 2;
+    *reinterpret_cast<uint32_t *>(th + mx_dword_off(i, d)) = (hlo >> 16) | (hhi << 16);
+    *reinterpret_cast<uint32_t *>(tl + mx_dword_off(i, d)) = (llo >> 16) | (lhi << 16);
+  }
+  if (g == 0) reinterpret_cast<float *>(s_rec + 4 * kMxTile)[s * 32 + i] = ok ? scale : 0.0f;
   __syncthreads();
-  // Per half-record: 96 x 16 bytes of tiles, then the 32 scales.
-  for (int e = threadIdx.x; e < kActJobs * 128; e += kThreads) {
-    const int j = e >> 7, w = e & 127;
-    const uint32_t u = blockIdx.x * kActJobs + j;
-    if (u >= units) continue;
-    const uint32_t tt = u / bp2, b = u % bp2;
-    uint8_t *rec = mxa + (static_cast<size_t>(tt) * pp + (b >> 1)) * kMxARec;
-    if (w < 96)
-      reinterpret_cast<uint4 *>(rec + 2 * (b & 1) * kMxTile)[w] = reinterpret_cast<const uint4 *>(s_tile[j])[w];
-    else
-      reinterpret_cast<float *>(rec + 4 * kMxTile)[(b & 1) * 32 + (w - 96)] = s_scale[j][w - 96];
-  }
+  constexpr int kChunks = static_cast<int>(kMxARec / 16);  // 208 16-byte chunks
+  if (tid < kChunks && r < recs)
+    reinterpret_cast<uint4 *>(mxa + static_cast<size_t>(r) * kMxARec)[tid] = reinterpret_cast<const uint4 *>(s_rec)[tid];
 }
 
 __global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__restrict__ aq,
@@ -409,11 +428,10 @@ hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const size_t units = mt * pp * 2;  // half-records; < 2^31: the image is below kMxMaxBytes
-  const unsigned wgs = blocks_for(units, kActJobs);
-  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(wgs), dim3(kThreads), 0, st, x, static_cast<int>(m),
-                     static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale,
-                     static_cast<uint32_t>(units), mxa);
+  const size_t recs = mt * pp;  // < 2^31: the image is below kMxMaxBytes
+  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(static_cast<unsigned>(recs)), dim3(kThreads), 0, st, x,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale,
+                     static_cast<uint32_t>(recs), mxa);
   return hipGetLastError();
 }
 
