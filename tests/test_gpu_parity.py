@@ -84,6 +84,34 @@ def test_gemv_nan_blocks_match_oracle(gpu_ctx, oracle):
     assert_close(y, ref)
 
 
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("m", [2, 20, 70, 130])
+def test_gemm_special_blocks_match_oracle(gpu_ctx, oracle, per_row, m):
+    """Every token-count route's activation quantizer (in the batch kernel, the MMA image, the
+    GEMM's fp6 image) on NaN blocks, a denormal block max (1/scale overflows: the reference's own
+    rounding path), exact .5 ties and zero blocks, against the oracle's GEMM.  No inf: 0 * inf
+    would make a row NaN."""
+    n, k = 97, 512
+    rows = []
+    for t in range(m):
+        x = _nan_blocks(k, 60 + t)
+        x[128:160] = 0.5 * (t % 3)        # zero block for every third token
+        x[160:168] = [127.0, 2.5, -2.5, 0.5, -0.5, 126.5, -1.5, 3.5]  # ties (amax 127: scale 1)
+        x[168:192] = 0.0
+        rows.append(x if t % 2 == 0 else x[::-1].copy())
+    x = _f32(np.stack(rows))
+    b = synth.q4_blocks(61 + m, n, k)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        got = np.zeros((m, n), dtype=np.float32)
+        q4.gemm_q4(q4.Q4Matrix.from_blocks(n, k, b, gpu_ctx), x, got, m)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    ref = oracle.gemm_q4(oracle.Q4Matrix(n, k, b), x, m, per_row=per_row, threads=8)
+    assert np.isfinite(ref).all()
+    assert_close(got, ref, what=f"m={m}")
+
+
 # ---- gemv_q4_prep and the device act-quant ---------------------------------------------
 @pytest.mark.parametrize("per_row", [False, True])
 @pytest.mark.parametrize("n,k", [(8192, 1536), (1536, 8192), (70, 96), (33, 32 * 33), (5, 32768), (300, 65536),
