@@ -498,24 +498,29 @@ struct MmaChunk {
 // Issue every load of chunk ch: weights (piece p = 64 i + lane is row p / CB,
 // block p % CB), weight scales (row lane / 4, blocks SL (lane % 4) + e), then
 // each token tile's B operands and scales from the activation image (one
-// contiguous 1 KB / 256 B run per instruction).
-template <int TT, int CB>
+// contiguous 1 KB / 256 B run per instruction).  PART 1 issues only the
+// weight loads (all zeros when `valid` is false), PART 2 only the
+// activation loads.
+template <int TT, int CB, int PART = 0>
 __device__ __forceinline__ void mma_load(const Q4MmaArgs &a, __amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t sr,
                                          __amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t ar, int ch,
-                                         MmaChunk<TT, CB> &c) {
+                                         MmaChunk<TT, CB> &c, bool valid = true) {
   using C = MmaChunk<TT, CB>;
   const int lane = threadIdx.x & 63, lr = lane & 15;
-  const int bpr = a.bpr, kb0 = ch * CB;
+  const int bpr = a.bpr, kb0 = ch * CB, kb_end = valid ? bpr : 0;
+  if constexpr (PART != 2) {
 #pragma unroll
-  for (int i = 0; i < C::WL; i++) {
-    const int p = 64 * i + lane, r = p / CB, kb = kb0 + p % CB;
-    c.wv[i] = buf_load16<kAuxNT>(wr, kb < bpr ? static_cast<uint32_t>(r * bpr + kb) * 16u : kOOB);
-  }
+    for (int i = 0; i < C::WL; i++) {
+      const int p = 64 * i + lane, r = p / CB, kb = kb0 + p % CB;
+      c.wv[i] = buf_load16<kAuxNT>(wr, kb < kb_end ? static_cast<uint32_t>(r * bpr + kb) * 16u : kOOB);
+    }
 #pragma unroll
-  for (int e = 0; e < C::SL; e++) {
-    const int r = lane >> 2, kb = kb0 + C::SL * (lane & 3) + e;
-    c.sv[e] = buf_load_u16(sr, kb < bpr ? static_cast<uint32_t>(r * bpr + kb) * 2u : kOOB);
+    for (int e = 0; e < C::SL; e++) {
+      const int r = lane >> 2, kb = kb0 + C::SL * (lane & 3) + e;
+      c.sv[e] = buf_load_u16(sr, kb < kb_end ? static_cast<uint32_t>(r * bpr + kb) * 2u : kOOB);
+    }
   }
+  if constexpr (PART == 1) return;
 #pragma unroll
   for (int tt = 0; tt < TT; tt++) {
     const bool tile = tt < a.mt;
@@ -610,7 +615,7 @@ __device__ __forceinline__ void mma_compute(const MmaChunk<TT, CB> &c, uint32_t 
 // W = RG x KW waves: RG row groups of 16 rows, KW K slices.  The planner
 // gives each wave one chunk when the row allows it, so all of a wave's loads
 // are in flight at once (the GEMV's single round trip); longer rows loop.
-template <int TT, int KW, int CB, int RG>
+template <int TT, int KW, int CB, int RG, bool PF = false>
 __global__ __launch_bounds__(RG * KW * 64) void q4_mma_kernel(Q4MmaArgs a) {
   constexpr int W = RG * KW;
   constexpr int RS = CB * 4 + 4;
@@ -640,10 +645,38 @@ __global__ __launch_bounds__(RG * KW * 64) void q4_mma_kernel(Q4MmaArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; v++) acc[tt][v] = 0.0f;
 
-  for (int ch = ch_lo; ch < ch_hi; ch++) {
+  // PF (one token tile over three or more chunks per wave): the next chunk's
+  // weights are requested right after this chunk's activation operands (the
+  // fences keep that order, so waiting for the operands leaves them in
+  // flight), and their HBM round trip overlaps this chunk's work.  Whole
+  // calls, interleaved A/B, bit-identical: M=16, K=8192, N=1536 10.7 -> 10.1
+  // us; M=12, K=16384, N=2048 17.5 -> 15.6 us; M=5, K=8192, N=4096 11.6 ->
+  // 11.0 us.  Over one or two chunks per wave it cost 5-9% (M=16, K=2048,
+  // N=8192; M=8, K=4096, N=8192), and with two to four token tiles it was
+  // mixed (the three-tile kernel drops to 3 waves per SIMD), so those load
+  // chunk by chunk, in a kernel of their own (sharing one with the PF loop
+  // cost the one-chunk launches 4%).
+  if constexpr (PF) {
     MmaChunk<TT, CB> c;
-    mma_load<TT, CB>(a, wr, sr, cr, ar, ch, c);
-    mma_compute<TT, CB>(c, s_w[wave], s_sw[wave], acc);
+    mma_load<TT, CB, 1>(a, wr, sr, cr, ar, ch_lo, c, ch_lo < ch_hi);
+    for (int ch = ch_lo; ch < ch_hi; ch++) {
+      mma_load<TT, CB, 2>(a, wr, sr, cr, ar, ch, c);
+      __builtin_amdgcn_sched_barrier(0);
+      MmaChunk<TT, CB> nx;
+      mma_load<TT, CB, 1>(a, wr, sr, cr, ar, ch + 1, nx, ch + 1 < ch_hi);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_compute<TT, CB>(c, s_w[wave], s_sw[wave], acc);
+#pragma unroll
+      for (int i = 0; i < MmaChunk<TT, CB>::WL; i++) c.wv[i] = nx.wv[i];
+#pragma unroll
+      for (int e = 0; e < MmaChunk<TT, CB>::SL; e++) c.sv[e] = nx.sv[e];
+    }
+  } else {
+    for (int ch = ch_lo; ch < ch_hi; ch++) {
+      MmaChunk<TT, CB> c;
+      mma_load<TT, CB>(a, wr, sr, cr, ar, ch, c);
+      mma_compute<TT, CB>(c, s_w[wave], s_sw[wave], acc);
+    }
   }
 
   // K slices meet in LDS and are added in slice order; D layout: token
@@ -681,6 +714,12 @@ template <int TT, int KW, int CB, int RG>
 hipError_t launch_mma(const Q4MmaArgs &a, hipStream_t st) {
   const int rows_per_wg = 16 * RG;
   const unsigned wgs = static_cast<unsigned>((a.n + rows_per_wg - 1) / rows_per_wg);
+  if constexpr (TT == 1) {
+    if ((a.bpr + CB - 1) / CB / KW >= 3) {  // every K slice has >= 3 chunks
+      hipLaunchKernelGGL((q4_mma_kernel<TT, KW, CB, RG, true>), dim3(wgs), dim3(RG * KW * 64), 0, st, a);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((q4_mma_kernel<TT, KW, CB, RG>), dim3(wgs), dim3(RG * KW * 64), 0, st, a);
   return hipGetLastError();
 }
