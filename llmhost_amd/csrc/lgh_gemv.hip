@@ -645,17 +645,19 @@ __global__ __launch_bounds__(RG * KW * 64) void q4_mma_kernel(Q4MmaArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; v++) acc[tt][v] = 0.0f;
 
-  // PF (one token tile over three or more chunks per wave): the next chunk's
-  // weights are requested right after this chunk's activation operands (the
-  // fences keep that order, so waiting for the operands leaves them in
-  // flight), and their HBM round trip overlaps this chunk's work.  Whole
-  // calls, interleaved A/B, bit-identical: M=16, K=8192, N=1536 10.7 -> 10.1
-  // us; M=12, K=16384, N=2048 17.5 -> 15.6 us; M=5, K=8192, N=4096 11.6 ->
-  // 11.0 us.  Over one or two chunks per wave it cost 5-9% (M=16, K=2048,
-  // N=8192; M=8, K=4096, N=8192), and with two to four token tiles it was
-  // mixed (the three-tile kernel drops to 3 waves per SIMD), so those load
-  // chunk by chunk, in a kernel of their own (sharing one with the PF loop
-  // cost the one-chunk launches 4%).
+  // PF (one or four token tiles over three or more chunks per wave): the
+  // next chunk's weights are requested right after this chunk's activation
+  // operands (the fences keep that order, so waiting for the operands leaves
+  // them in flight), and their HBM round trip overlaps this chunk's work.
+  // Whole calls, interleaved A/B, bit-identical: M=16, K=8192, N=1536 10.7 ->
+  // 10.1 us; M=12, K=16384, N=2048 17.5 -> 15.6 us; M=5, K=8192, N=4096 11.6
+  // -> 11.0 us; M=64, K=8000, N=8192 36.5 -> 34.3 us; M=64, K=6144, N=4096
+  // 18.0 -> 16.7 us.  Over one or two chunks per wave it cost 5-9% (M=16,
+  // K=2048, N=8192; M=8, K=4096, N=8192); three token tiles lost 2-4% (M=40
+  // and 48 at K=4096-8192), and two lost up to 9% on large grids (M=30,
+  // K=8192, N=16384: 88 -> 170 VGPRs), so those load chunk by chunk, in a
+  // kernel of their own (sharing one with the PF loop cost the one-chunk
+  // launches 4%).
   if constexpr (PF) {
     MmaChunk<TT, CB> c;
     mma_load<TT, CB, 1>(a, wr, sr, cr, ar, ch_lo, c, ch_lo < ch_hi);
@@ -714,7 +716,7 @@ template <int TT, int KW, int CB, int RG>
 hipError_t launch_mma(const Q4MmaArgs &a, hipStream_t st) {
   const int rows_per_wg = 16 * RG;
   const unsigned wgs = static_cast<unsigned>((a.n + rows_per_wg - 1) / rows_per_wg);
-  if constexpr (TT == 1) {
+  if constexpr (TT == 1 || TT == 4) {
     if ((a.bpr + CB - 1) / CB / KW >= 3) {  // every K slice has >= 3 chunks
       hipLaunchKernelGGL((q4_mma_kernel<TT, KW, CB, RG, true>), dim3(wgs), dim3(RG * KW * 64), 0, st, a);
       return hipGetLastError();

@@ -421,13 +421,13 @@ def test_gemm_matches_oracle(gpu_ctx, oracle, m, n, k):
                                    (24, 129, 4096), (48, 77, 1056), (64, 40, 8192), (33, 16, 544),
                                    (40, 77, 1568), (33, 8192, 2048), (48, 130, 8192), (35, 8191, 1536),
                                    (45, 8193, 1536), (16, 1536, 8192), (7, 100, 16384), (13, 200, 4128),
-                                   (11, 300, 6816)])
+                                   (11, 300, 6816), (64, 300, 8000), (56, 130, 7168)])
 def test_small_batch_gemv_path(gpu_ctx, oracle, per_row, m, n, k):
     """2 <= m <= 64: the dot4 batch kernel (m <= 4) and the MFMA batch kernel (1 to 4 token
     tiles of 16, 1/2/4/8 K slices, 8-block chunks, and 4-block chunks for three token tiles over
-    rows of >= 48 blocks and <= 8192 rows, ragged chunk tails; one token tile over 3-16 chunks
-    per wave, uneven slices and a partial last chunk included, with the next chunk's weights in
-    flight), Assign and AddF64."""
+    rows of >= 48 blocks and <= 8192 rows, ragged chunk tails; one or four token tiles over 3-16
+    chunks per wave, uneven slices and a partial last chunk included, with the next chunk's
+    weights in flight), Assign and AddF64."""
     blocks = synth.q4_blocks(m + n + k, n, k)
     x = synth.activations(m * 7 + k, m, k)
     y0 = synth.activations(n + 5, m, n)
