@@ -151,7 +151,10 @@ size_t lgh_q4_device_bytes(const lgh_q4 *w);
  * this library's own (a file container around it: llmhost_amd/packfile.py);
  * it stands in for the pre-packed .lfmb container llm-quant plans
  * (ARCHITECTURE.md:101) and for Q4Matrix::from_blocks' per-load repack
- * (crates/llm-cpu/src/gemv_q4.rs:128-149). */
+ * (crates/llm-cpu/src/gemv_q4.rs:128-149).  Import copies the bytes as they
+ * are: a container stores lgh_image_layout() beside its images and loads
+ * them only into a library that returns the same value. */
+uint32_t lgh_image_layout(void);
 size_t lgh_q4_image_bytes(const lgh_q4 *w, int with_gemm);
 int lgh_q4_export(lgh_ctx *ctx, const lgh_q4 *w, int with_gemm, void *dst, size_t bytes);
 int lgh_q4_import(lgh_ctx *ctx, const void *src, size_t bytes, size_t n, size_t k, int with_gemm, lgh_q4 **out);
@@ -212,22 +215,40 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
 
 /* The same product as lgh_q4_gemm_dev, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc.  No counterpart in the reference (llm-cpu allocates
- * its activation buffers per call, gemv_q4.rs:725-798).  Every scratch buffer
- * of the call (activation images and codes, split-K partials) comes from one
- * fixed device array of LGH_NOALLOC_SCRATCH_BYTES per GPU, held until the
- * process ends; the call allocates, frees and synchronizes nothing.  Token
- * chunks shrink until their scratch fits; a call whose 32-token chunk still
- * needs more returns LGH_ERR_SHAPE.  Routes that need the matrix's GEMM image
- * return LGH_ERR_INVALID_ARG unless lgh_q4_prepare_gemm has built it (a
- * matrix too large for one needs none: its chunks of <= 64 tokens, 16 when
- * the row is too long for 64, run on the nibble planes).  Every
- * context on a GPU shares that GPU's array and it keeps the last call's
- * contents: calls that overlap on one GPU (several contexts or streams)
- * race, so the caller serializes them.  Results equal lgh_q4_gemm_dev's. */
+ * that forbid hipMalloc.  It has no counterpart in the reference.  Every
+ * scratch buffer of the call (activation images and codes, split-K partials)
+ * comes from one fixed device array of LGH_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends; the call allocates, frees and synchronizes
+ * nothing.  On the GEMM route (65 or more tokens) token chunks shrink until
+ * their scratch fits, keeping the split-K count of the whole call; a call
+ * whose 32-token chunk still needs more returns LGH_ERR_SHAPE.  The routes of
+ * 1-64 tokens (and the 64-token chunks of a matrix too large for a GEMM
+ * image) take their scratch in one piece and return LGH_ERR_SHAPE when it
+ * exceeds the array (only rows of more than about 466k elements can).
+ * Routes that need the matrix's GEMM image return LGH_ERR_INVALID_ARG unless
+ * lgh_q4_prepare_gemm has built it.  Every context on a GPU shares that GPU's
+ * array and it keeps the last call's contents: calls that overlap on one GPU
+ * (several contexts or streams) race, so the caller serializes them.
+ * Results equal lgh_q4_gemm_dev's bit for bit. */
 #define LGH_NOALLOC_SCRATCH_BYTES (32u << 20)
 int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m,
                             int mode);
+
+/* ---- measurement probes ----------------------------------------------------
+ * No counterpart in the reference.  Two launches that bound what any launch
+ * of the library can reach, for a benchmark to time in the same harness as
+ * the matmuls (device pointers, asynchronous on the context stream):
+ * lgh_probe_empty_dev launches an empty kernel of `workgroups` x 256 threads
+ * (1..65535) -- the per-launch floor of dependent launches;
+ * lgh_probe_read_dev reads `bytes` (a multiple of 16, below 2 GiB) at src_dev
+ * (16-byte aligned) with per_thread (1, 2, 4 or 8) 128-bit streaming loads per
+ * thread, all issued before any is used, and writes one f32 sum per
+ * workgroup to out_dev
+ * (lgh_probe_read_outputs(bytes, per_thread) floats; 0 for a bad per_thread)
+ * -- a plain streaming read of that size. */
+int lgh_probe_empty_dev(lgh_ctx *ctx, int workgroups);
+size_t lgh_probe_read_outputs(size_t bytes, int per_thread);
+int lgh_probe_read_dev(lgh_ctx *ctx, const void *src_dev, size_t bytes, int per_thread, float *out_dev);
 
 /* ---- Q8_0 GEMV ------------------------------------------------------------
  * q8_apply (crates/llm-engine/src/weights.rs:194-227), reached through

@@ -54,6 +54,7 @@ SIGNATURES = {
     "lgh_q4_download": (_I, [_P, _P, _P]),
     "lgh_q4_prepare_gemm": (_I, [_P, _P]),
     "lgh_q4_device_bytes": (_SZ, [_P]),
+    "lgh_image_layout": (C.c_uint32, []),
     "lgh_q4_image_bytes": (_SZ, [_P, _I]),
     "lgh_q4_export": (_I, [_P, _P, _I, _P, _SZ]),
     "lgh_q4_import": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, C.POINTER(_P)]),
@@ -76,6 +77,9 @@ SIGNATURES = {
     "lgh_q4_gemm": (_I, [_P, _P, _P, _P, _SZ, _I]),
     "lgh_q4_gemm_dev": (_I, [_P, _P, _P, _P, _SZ, _I]),
     "lgh_q4_gemm_dev_noalloc": (_I, [_P, _P, _P, _P, _SZ, _I]),
+    "lgh_probe_empty_dev": (_I, [_P, _I]),
+    "lgh_probe_read_outputs": (_SZ, [_SZ, _I]),
+    "lgh_probe_read_dev": (_I, [_P, _P, _SZ, _I, _P]),
     "lgh_q8_gemv": (_I, [_P, _P, _P, _P, _SZ]),
     "lgh_q8_gemv_dev": (_I, [_P, _P, _P, _P, _SZ]),
     "lgh_act_quant": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libllm_gpu_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["lgh_api.hip", "lgh_gemv.hip", "lgh_gemm.hip", "lgh_quant.hip", "lgh_ffn.hip"]
+SOURCES = ["lgh_api.hip", "lgh_gemv.hip", "lgh_gemm.hip", "lgh_quant.hip", "lgh_ffn.hip", "lgh_probe.hip"]
 ARCH = "gfx950"
 
 # Packed FP32 VALU ops are disabled on purpose: every kernel here is written

@@ -491,6 +491,8 @@ int lgh_q4_download(lgh_ctx *ctx, const lgh_q4 *w, void *blocks) {
 }
 
 // ---- device images: the matrix as it sits in HBM, for a load that is one copy ----
+uint32_t lgh_image_layout(void) { return lgh::kImageLayout; }
+
 size_t lgh_q4_image_bytes(const lgh_q4 *w, int with_gemm) {
   if (!w) return 0;
   const size_t nb = w->n * w->bpr;
@@ -763,8 +765,8 @@ int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, co
     auto *mxa = reinterpret_cast<uint8_t *>(ws + o_mx);
     LGH_HIP(ctx, lgh::launch_act_split_mx(qs_dev, scales_dev, 1, w->k, mxa, ctx->stream));
     float *ys[1] = {y_dev};
-    LGH_HIP(ctx, lgh::launch_q4_gemm(ws1, 1, mxa, ys, 1, mode, reinterpret_cast<float *>(ws + o_part), part_floats,
-                                     ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemm(ws1, 1, mxa, ys, 1, mode, splits, reinterpret_cast<float *>(ws + o_part),
+                                     part_floats, ctx->stream));
     return LGH_OK;
   }
   LGH_HIP(ctx, lgh::launch_q4_gemv_codes(w, qs_dev, scales_dev, y_dev, mode, ctx->stream));
@@ -839,12 +841,12 @@ static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int 
     l.bytes = cv.off;
     return l;
   };
-  size_t chunk = std::min<size_t>(m, 64);
-  Layout lay = layout(chunk);
-  while (lay.bytes > wsp.limit() && chunk > 16) {
-    chunk = std::max<size_t>(16, chunk / 2 / 16 * 16);
-    lay = layout(chunk);
-  }
+  // 64 tokens per launch whatever the scratch: the kernel's plan (token
+  // tiles, K slices) depends on the chunk, so a smaller chunk could change
+  // the f32 summation order.  A fixed scratch too small for the chunk's image
+  // fails in wsp.get.
+  const size_t chunk = std::min<size_t>(m, 64);
+  const Layout lay = layout(chunk);
   char *ws = nullptr;
   if (int r = wsp.get(lay.bytes, &ws)) return r;
   auto *ci = reinterpret_cast<uint8_t *>(ws + lay.o_ci);
@@ -938,14 +940,18 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
   if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", k);
   size_t rows = 0;
   for (int j = 0; j < nmat; j++) rows += w[j]->n;
+  // The split count sets the order of the f32 additions, so it is planned
+  // once, for the token chunk the allocating path takes, and kept when the
+  // fixed scratch forces smaller chunks: chunking changes only the scratch
+  // footprint, never the result.
+  const size_t chunk0 = std::min(m, (cap_tiles - 8) * 32);
+  const int splits = lgh::plan_q4_gemm_splits(w, nmat, chunk0);
   struct Layout {
-    int splits;
     size_t part_floats, o_mx, o_rs, o_part, bytes;
   };
   auto layout = [&](size_t c) {
     Layout l{};
-    l.splits = lgh::plan_q4_gemm_splits(w, nmat, c);
-    l.part_floats = l.splits > 1 ? static_cast<size_t>(l.splits) * c * rows : 0;
+    l.part_floats = splits > 1 ? static_cast<size_t>(splits) * c * rows : 0;
     Carve cv;
     l.o_mx = cv.take((c + 31) / 32 * rec_per_tile);
     l.o_rs = cv.take(c * sizeof(float));
@@ -953,7 +959,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     l.bytes = cv.off;
     return l;
   };
-  size_t chunk = std::min(m, (cap_tiles - 8) * 32);
+  size_t chunk = chunk0;
   Layout lay = layout(chunk);
   while (lay.bytes > wsp.limit() && chunk > 32) {  // halve, in whole 32-token tiles
     chunk = std::max<size_t>(32, (chunk / 2 + 31) / 32 * 32);
@@ -970,7 +976,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     float *yc[3] = {nullptr, nullptr, nullptr};
     for (int j = 0; j < nmat; j++) yc[j] = w[j]->n ? y_dev[j] + m0 * w[j]->n : nullptr;
     LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * k, mc, k, ctx->act_mode, mxa, rs, ctx->stream));
-    LGH_HIP(ctx, lgh::launch_q4_gemm(w, nmat, mxa, yc, mc, mode, part, part_floats, ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemm(w, nmat, mxa, yc, mc, mode, splits, part, part_floats, ctx->stream));
   }
   return LGH_OK;
 }
@@ -986,8 +992,10 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
 
 // lgh_q4_gemm_dev with every scratch buffer taken from the device's fixed
 // scratch array instead of the context workspace: no allocation, no free, no
-// synchronisation.  Token chunks shrink until their scratch fits; a call that
-// needs more than the array holds even for 32 tokens fails with LGH_ERR_SHAPE.
+// synchronisation.  On the GEMM route (65+ tokens) token chunks shrink until
+// their scratch fits, with the split count of the whole call; a call that
+// needs more than the array holds even for 32 tokens, or whose route takes
+// its scratch in one piece (1-64 tokens), fails with LGH_ERR_SHAPE.
 int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
   if (!ctx) return LGH_ERR_INVALID_ARG;
   if (int r = check_mat(ctx, w)) return r;
@@ -997,6 +1005,36 @@ int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, f
   if (!ctx->scratch) return fail(ctx, LGH_ERR_INVALID_ARG, "device %d has no fixed scratch", ctx->device);
   const Ws fixed{ctx, static_cast<char *>(ctx->scratch), LGH_NOALLOC_SCRATCH_BYTES};
   return gemm_multi_dev(ctx, fixed, &w, 1, x_dev, &y_dev, m, mode);
+}
+
+// ---- measurement probes ------------------------------------------------------------
+int lgh_probe_empty_dev(lgh_ctx *ctx, int workgroups) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (workgroups < 1 || workgroups > 65535)
+    return fail(ctx, LGH_ERR_INVALID_ARG, "workgroups %d outside 1..65535", workgroups);
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_probe_empty(workgroups, ctx->stream));
+  return LGH_OK;
+}
+
+size_t lgh_probe_read_outputs(size_t bytes, int per_thread) {
+  if (per_thread != 1 && per_thread != 2 && per_thread != 4 && per_thread != 8) return 0;
+  return lgh::probe_read_workgroups(bytes, per_thread);
+}
+
+int lgh_probe_read_dev(lgh_ctx *ctx, const void *src_dev, size_t bytes, int per_thread, float *out_dev) {
+  if (!ctx) return LGH_ERR_INVALID_ARG;
+  if (per_thread != 1 && per_thread != 2 && per_thread != 4 && per_thread != 8)
+    return fail(ctx, LGH_ERR_INVALID_ARG, "per_thread %d is not 1, 2, 4 or 8", per_thread);
+  if (bytes % 16) return fail(ctx, LGH_ERR_SHAPE, "%zu bytes is not a multiple of 16", bytes);
+  if (bytes == 0) return LGH_OK;
+  if (!src_dev || !out_dev) return fail(ctx, LGH_ERR_INVALID_ARG, "null source or output");
+  if (!aligned16(src_dev) || (reinterpret_cast<uintptr_t>(out_dev) & 3u))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "source must be 16-byte and output 4-byte aligned");
+  if (bytes >= (size_t{1} << 31)) return fail(ctx, LGH_ERR_SHAPE, "%zu bytes: the probe reads < 2 GiB", bytes);
+  if (int r = set_device(ctx)) return r;
+  LGH_HIP(ctx, lgh::launch_probe_read(src_dev, bytes, per_thread, out_dev, ctx->stream));
+  return LGH_OK;
 }
 
 int lgh_q8_gemv_dev(lgh_ctx *ctx, const lgh_q8 *w, const float *x_dev, float *y_dev, size_t tokens) {

@@ -560,13 +560,13 @@ int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m) {
 }
 
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
-                          float *part, size_t part_floats, hipStream_t st) {
+                          int splits, float *part, size_t part_floats, hipStream_t st) {
   if (m == 0 || nmat < 1 || nmat > 3) return m == 0 ? hipSuccess : hipErrorInvalidValue;
   size_t rows = 0;
   for (int j = 0; j < nmat; j++) rows += w[j]->n;
   if (rows == 0) return hipSuccess;
-  int splits = plan_q4_gemm_splits(w, nmat, m);
-  while (splits > 1 && static_cast<size_t>(splits) * m * rows > part_floats) splits /= 2;
+  if (splits < 1 || (splits > 1 && (!part || static_cast<size_t>(splits) * m * rows > part_floats)))
+    return hipErrorInvalidValue;
   const size_t mt = (m + 31) / 32;
   GemmMulti gm{};
   size_t off = 0;

@@ -86,6 +86,11 @@ constexpr size_t kMxWRec = 2 * kMxTile + 256;   // weights: 2 tiles + 64 f32 sca
 constexpr size_t kMxARec = 4 * kMxTile + 256;   // activations: 2 x {h, l} tiles + 64 f32
 // Buffer-load offsets are 32-bit: operand images must stay below this.
 constexpr size_t kMxMaxBytes = size_t(1) << 31;
+// Names the layout of the device images lgh_q4_export / lgh_q8_export write
+// and lgh_*_import copy back without checking: the revision of the plane
+// formats and the GEMM operand image (high 16 bits; raised whenever either
+// changes) and the weight record size (low 16 bits).
+constexpr uint32_t kImageLayout = (1u << 16) | static_cast<uint32_t>(kMxWRec);
 
 // Weight operand image from the repacked nibble/scale planes (load time).
 hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t stream);
@@ -209,12 +214,22 @@ hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int
 // GEMM on an activation operand image: y[j][m][n_j] (+)= x[m][k] . W[j]^T for
 // 1..3 matrices with the same k, one launch (the workgroups of all matrices
 // in one grid, one split-K reduce).  plan_q4_gemm_splits() is the number of K
-// splits the launch wants for m tokens; `part` holds part_floats floats of
-// scratch, and the launch uses fewer splits when splits * m * (sum of n)
-// would not fit.
+// splits a call of m tokens wants; the caller passes the count it planned
+// (the split count fixes the f32 summation order, so a call cut into token
+// chunks keeps the count of the whole call), and `part` must hold
+// splits * m * (sum of n) floats when splits > 1 (hipErrorInvalidValue
+// otherwise, nothing launched).
 int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m);
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
-                          float *part, size_t part_floats, hipStream_t stream);
+                          int splits, float *part, size_t part_floats, hipStream_t stream);
+
+// Measurement probes: an empty kernel of `wgs` workgroups, and a plain read
+// of `bytes` (a multiple of 16, 16-byte aligned) with per_thread (1, 2, 4, 8)
+// 16-byte loads per thread, one f32 sum per workgroup into out
+// [probe_read_workgroups(bytes, per_thread)].
+size_t probe_read_workgroups(size_t bytes, int per_thread);
+hipError_t launch_probe_empty(int wgs, hipStream_t stream);
+hipError_t launch_probe_read(const void *src, size_t bytes, int per_thread, float *out, hipStream_t stream);
 
 // Test hooks.
 hipError_t launch_q4_block_dots(const uint8_t *qs, const int8_t *a, size_t nblocks, int32_t *out,

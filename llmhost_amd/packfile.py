@@ -2,10 +2,12 @@
 with no quantization and no repack kernel.
 
 Layout (little-endian):  b"LGHB"  u32 version  u64 header_len  header (UTF-8 JSON)  data.
-The header maps each name to {"kind": "q4" | "q8", "n", "k", "gemm": bool, "offset", "bytes"};
-offsets are from the start of the data section and 256-byte aligned.  A tensor's bytes are the
-library's device image of the matrix (``lgh_q4_export`` / ``lgh_q8_export``): the nibble (or
-code) plane, the f16 scale plane and, for Q4 with "gemm", the GEMM operand image.
+The header holds "layout" (``lgh_image_layout()`` of the library that wrote the images) and maps
+each name to {"kind": "q4" | "q8", "n", "k", "gemm": bool, "offset", "bytes"}; offsets are from
+the start of the data section and 256-byte aligned.  A tensor's bytes are the library's device
+image of the matrix (``lgh_q4_export`` / ``lgh_q8_export``): the nibble (or code) plane, the f16
+scale plane and, for Q4 with "gemm", the GEMM operand image.  The library copies an image back
+without checking it, so a file whose layout differs from the loading library's is rejected.
 
 The reference loads safetensors and quantizes at load (crates/llm-engine/src/load.rs:120-191,
 Q4Matrix::from_blocks repacking every load, crates/llm-cpu/src/gemv_q4.rs:128-149) and plans a
@@ -25,8 +27,13 @@ from . import q4 as _q4
 from ._ffi import LghShapeError, LGH_ERR_SHAPE, lib
 
 MAGIC = b"LGHB"
-VERSION = 1
+VERSION = 2
 ALIGN = 256
+
+
+def image_layout() -> int:
+    """The device image layout of the loaded library (``lgh_image_layout``)."""
+    return int(lib().lgh_image_layout())
 
 
 def _align(v: int) -> int:
@@ -63,14 +70,17 @@ def import_image(kind: str, image: np.ndarray, n: int, k: int, with_gemm: bool =
     raise ValueError(f"unknown matrix kind {kind!r}")
 
 
-def write_raw(path: str, entries: dict) -> None:
-    """Write already-exported images: entries[name] = (kind, n, k, gemm, uint8 image)."""
+def write_raw(path: str, entries: dict, layout: int | None = None) -> None:
+    """Write already-exported images: entries[name] = (kind, n, k, gemm, uint8 image), made by a
+    library whose ``lgh_image_layout()`` is ``layout`` (default: the loaded library's)."""
+    layout = image_layout() if layout is None else int(layout)
     header, off = {}, 0
     for name, (kind, n, k, gemm, img) in entries.items():
         header[name] = {"kind": kind, "n": int(n), "k": int(k), "gemm": bool(gemm), "offset": off,
                         "bytes": int(img.size)}
         off = _align(off + img.size)
-    hj = json.dumps({"format": "lghb", "version": VERSION, "tensors": header}, sort_keys=True).encode()
+    hj = json.dumps({"format": "lghb", "version": VERSION, "layout": layout, "tensors": header},
+                    sort_keys=True).encode()
     pre = MAGIC + struct.pack("<IQ", VERSION, len(hj)) + hj
     data_start = _align(len(pre))
     with open(path, "wb") as f:
@@ -98,6 +108,9 @@ def read_index(path: str):
     if len(hj) != hlen:
         raise LghShapeError(LGH_ERR_SHAPE, f"{path}: truncated header")
     meta = json.loads(hj)
+    if meta.get("layout") != image_layout():
+        raise LghShapeError(LGH_ERR_SHAPE, f"{path}: images of layout {meta.get('layout')!r}, this "
+                            f"library reads layout {image_layout()}; export the matrices again")
     start = _align(16 + hlen)
     for name, t in meta["tensors"].items():
         if t["offset"] % ALIGN or start + t["offset"] + t["bytes"] > size:

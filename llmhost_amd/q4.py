@@ -379,6 +379,28 @@ def _gemm(w: Q4Matrix, x, out, m: int, mode: int) -> None:
     ctx.check(lib().lgh_q4_gemm(ctx.handle, w.handle, _np_ptr(x), _np_ptr(out), m, mode))
 
 
+def probe_empty(workgroups: int = 1, ctx: Context | None = None) -> None:
+    """One launch of an empty kernel of `workgroups` x 256 threads (lgh_probe_empty_dev), in torch's
+    stream order: the per-launch floor a benchmark times beside the matmuls."""
+    ctx = ctx or default_context()
+    ctx.dev_call(lambda: ctx.check(lib().lgh_probe_empty_dev(ctx.handle, int(workgroups))))
+
+
+def probe_read(src, out, per_thread: int = 4, ctx: Context | None = None) -> None:
+    """A plain streaming read of the device tensor `src` (lgh_probe_read_dev): one f32 sum per
+    workgroup into the device tensor `out` (``probe_read_outputs`` floats)."""
+    ctx = ctx or default_context()
+    nbytes = src.numel() * src.element_size()
+    need = probe_read_outputs(nbytes, per_thread)
+    sp, op = _dev_ptr_of(src, "src", src.dtype), _dev_ptr(out, "out")
+    _shape_assert(out.numel() >= need, f"out holds {out.numel()} floats, the read writes {need}")
+    ctx.dev_call(lambda: ctx.check(lib().lgh_probe_read_dev(ctx.handle, sp, nbytes, int(per_thread), op)))
+
+
+def probe_read_outputs(nbytes: int, per_thread: int = 4) -> int:
+    return int(lib().lgh_probe_read_outputs(nbytes, int(per_thread)))
+
+
 def gemv_q4(w: Q4Matrix, x, out) -> None:
     """`out[n] = W[n, k] @ x[k]` with on-the-fly Q8 activations (gemv_q4.rs:344-352)."""
     _gemm(w, x, out, 1, _ffi.LGH_ASSIGN)

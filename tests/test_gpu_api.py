@@ -189,3 +189,28 @@ def test_null_matrix_is_an_error_on_every_matrix_entry_point(gpu_ctx):
         assert b"null matrix 1" in L.lgh_last_error(h)
     finally:
         w.free()
+
+
+@pytest.mark.parametrize("per_thread", [1, 2, 4, 8])
+def test_probe_read_sums_what_it_reads(gpu_ctx, per_thread):
+    """The streaming-read probe that benchmarks time beside the GEMVs reads every byte it is given:
+    its per-workgroup sums match float64 sums of the same 4 KB * per_thread chunks (a ragged last
+    chunk included), and the empty-kernel probe runs."""
+    import torch
+
+    print(f"[probe] per_thread={per_thread}", flush=True)
+    nbytes = 7116800 + 48  # not a whole number of workgroup chunks
+    src = torch.randn(nbytes // 4, device="cuda")
+    nout = q4.probe_read_outputs(nbytes, per_thread)
+    chunk = 256 * 16 * per_thread
+    assert nout == (nbytes + chunk - 1) // chunk
+    out = torch.full((nout + 1,), float("nan"), device="cuda")
+    q4.probe_read(src, out, per_thread, gpu_ctx)
+    q4.probe_empty(256, gpu_ctx)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    ref = np.add.reduceat(src.cpu().numpy().astype(np.float64), np.arange(0, nbytes // 4, chunk // 4))
+    assert np.isnan(got[nout])  # nothing past the last workgroup's output
+    np.testing.assert_allclose(got[:nout], ref, rtol=1e-5, atol=1e-3)
+    with pytest.raises(q4.LghError):
+        q4.probe_read(src, out, 3, gpu_ctx)

@@ -36,3 +36,17 @@ def test_damaged_files_are_rejected(tmp_path):
         f.write(data[:-10])
     with pytest.raises(LghShapeError, match="outside the file"):
         packfile.read_index(trunc)
+
+
+def test_images_of_another_layout_are_rejected(tmp_path):
+    """The library copies an image back unchecked, so a file written for another image layout
+    (a stale GEMM record format) must not load."""
+    lay = packfile.image_layout()
+    assert lay & 0xFFFF == 1792  # the GEMM weight record size
+    p = str(tmp_path / "old.lghb")
+    packfile.write_raw(p, {"x": ("q4", 1, 32, False, np.zeros(18, np.uint8))}, layout=lay + (1 << 16))
+    with pytest.raises(LghShapeError, match="layout"):
+        packfile.read_index(p)
+    ok = str(tmp_path / "ok.lghb")
+    packfile.write_raw(ok, {"x": ("q4", 1, 32, False, np.zeros(18, np.uint8))})
+    assert packfile.read_index(ok)[0]["x"]["bytes"] == 18

@@ -28,6 +28,7 @@ CASES = [
     (10752, 2048, 512, 130),    # fp6 GEMM, no split
     (2048, 10752, 512, 100),    # fp6 GEMM with split-K partials in scratch
     (2048, 10752, 2048, 1100),  # GEMM whose 2048-token image exceeds the array: token chunks
+    (512, 8192, 4096, 2100),    # chunks of fewer tiles keep the whole call's split count (none)
     (512, 65536, 1, 1),         # M=1 with K > 32768: the GEMM route
 ]
 
@@ -87,6 +88,23 @@ def test_noalloc_rejects_scratch_beyond_the_array(gpu_ctx):
     assert (k // 64) * 3328 * 1 > SCRATCH
     w = q4.Q4Matrix.from_blocks(n, k, synth.q4_blocks(3401, n, k), gpu_ctx)
     w.prepare_gemm()
+    x = torch.zeros(m, k, device="cuda")
+    y = torch.zeros(m, n, device="cuda")
+    torch.cuda.synchronize()
+    lib = _ffi.lib()
+    with pytest.raises(q4.LghShapeError, match="fixed scratch"):
+        _call(lib.lgh_q4_gemm_dev_noalloc, gpu_ctx, w, x, y, m, _ffi.LGH_ASSIGN)
+    w.free()
+
+
+def test_noalloc_rejects_mma_scratch_beyond_the_array(gpu_ctx):
+    """40 tokens take the matrix-core batch route, whose activation image is taken in one piece:
+    at K = 640000 it needs 3 token tiles x 5000 block quads x 2304 B = 34.6 MB > 32 MiB."""
+    import torch
+
+    n, k, m = 16, 640000, 40
+    assert 3 * (k // 128) * (2048 + 256) > SCRATCH
+    w = q4.Q4Matrix.from_blocks(n, k, synth.q4_blocks(3501, n, k), gpu_ctx)
     x = torch.zeros(m, k, device="cuda")
     y = torch.zeros(m, n, device="cuda")
     torch.cuda.synchronize()
