@@ -347,6 +347,56 @@ def ffn_case(gb: GpuBench, iters, dim=1536, inter=8192):
             "bytes": byts, "launches": 2}
 
 
+def ffn_prefill_case(gb: GpuBench, iters, dim=1536, inter=8192, tokens=512):
+    """Prefill FFN residual block (lfm2.rs:861-881) over `tokens` rows: the entry point, whose
+    gate/up activation image forms rms_norm(hidden) and whose down-projection image forms
+    silu(g) * u, against the op sequence it replaces (rms_norm; the gate/up pair on one shared
+    activation quantization; silu_mul; the down GEMM added in f64).  Rotating weight sets > 2x
+    MALL, GEMM images built before capture; hidden accumulates the residual across calls (the
+    norm keeps every call's input at unit RMS)."""
+    torch, q4 = gb.torch, gb.q4
+    from llmhost_amd import synth
+
+    set_bytes = 2 * inter * (dim // 32) * 18 + dim * (inter // 32) * 18
+    count = math.ceil((2 * MALL_BYTES + (64 << 20)) / set_bytes)
+    shapes = [(inter, dim), (inter, dim), (dim, inter)]
+    raws = [torch.from_numpy(synth.q4_blocks(620 + j, n, k).view(np.uint8).copy()).cuda()
+            for j, (n, k) in enumerate(shapes)]
+    sets = [[q4.Q4Matrix.from_blocks(n, k, raws[j], gb.ctx) for j, (n, k) in enumerate(shapes)]
+            for _ in range(count)]
+    del raws
+    for ws in sets:
+        for w in ws:
+            w.prepare_gemm()
+    hidden = torch.from_numpy(synth.activations(630, tokens, dim).ravel()).cuda()
+    nw = torch.from_numpy((1 + 0.1 * synth.normal_f32(631, dim)).astype(np.float32)).cuda()
+    normed = torch.zeros(tokens * dim, device="cuda")
+    g = torch.zeros(tokens * inter, device="cuda")
+    u = torch.zeros(tokens * inter, device="cuda")
+
+    def fused(i):
+        w1, w3, w2 = sets[i % count]
+        q4.ffn_residual(w1, w3, w2, nw, 1e-5, hidden, tokens)
+
+    def sequence(i):
+        w1, w3, w2 = sets[i % count]
+        q4.rms_norm(hidden, nw, 1e-5, normed, gb.ctx)
+        q4.norm_gemv([w1, w3], None, 1e-5, normed, [g, u], tokens)
+        q4.silu_mul(g, u, gb.ctx)
+        q4.gemm_q4_add(w2, g, hidden, tokens)
+
+    s_f = gb.timed(fused, iters, 3, reps=5)
+    s_s = gb.timed(sequence, iters, 3, reps=5)
+    for ws in sets:
+        for w in ws:
+            w.free()
+    ms_f, ms_s = statistics.median(s_f), statistics.median(s_s)
+    ops = 2.0 * tokens * dim * inter * 3
+    return {"dim": dim, "inter": inter, "tokens": tokens, "us": ms_f * 1e3, "tops": ops / (ms_f * 1e-3) / 1e12,
+            "frac_int8": ops / (ms_f * 1e-3) / 1e12 / INT8_PEAK_TOPS, "op_sequence_us": ms_s * 1e3,
+            "samples_us": [round(t * 1e3, 3) for t in s_f], "op_sequence_samples_us": [round(t * 1e3, 3) for t in s_s]}
+
+
 def block_input_case(gb: GpuBench, iters, rows, dim=1536, tokens=1):
     """Input side of an attention or conv block (lfm2.rs:784-794 / 651-659; prefill 698-711):
     rms_norm of `tokens` rows of hidden, then the block's projections (rows: the matrices' row
@@ -795,6 +845,8 @@ def main():
         extra["attn_qkv_dim1536"] = block_input_case(gb, 100, (1536, 512, 512))
         extra["conv_in_proj_dim1536"] = block_input_case(gb, 100, (4608,))
         extra["attn_qkv_dim1536_prefill_m512"] = block_input_case(gb, 10, (1536, 512, 512), tokens=512)
+        log("[bench] prefill FFN block (norm and silu * u fused into the activation images vs op sequence)")
+        extra["ffn_block_dim1536_inter8192_prefill_m512"] = ffn_prefill_case(gb, 10)
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")

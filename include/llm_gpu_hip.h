@@ -292,9 +292,13 @@ int lgh_silu_mul_dev(lgh_ctx *ctx, float *g_dev, const float *u_dev, size_t n);
  *   hidden = (float)((double)hidden + (double)(W2 h))   (gemv_q4_add / gemm_q4_add)
  * W1, W3: [inter, dim]; W2: [dim, inter].  Both activation quantizations
  * follow the context's act-quant mode.  One token with dim <= 2048 runs two
- * fused launches (the second reads h's ActQ8 codes written by the first);
- * otherwise the ops above run one after another on the device.  No single
- * reference function: it replaces the reference's sequence of calls. */
+ * fused launches (the second reads h's ActQ8 codes written by the first).
+ * Otherwise the ops above run on the device one after another, except that
+ * for 5 or more tokens the activation-image kernels of the two GEMMs form
+ * the norm (from per-row scales, without writing the normed rows) and
+ * silu(g) * u themselves; the results equal the op sequence's bit for bit.
+ * No single reference function: it replaces the reference's sequence of
+ * calls. */
 int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
                         const float *norm_w, float eps, float *hidden, size_t tokens);
 int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
@@ -311,7 +315,9 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
  * [tokens, W[j].n].  One token with k <= 2048 runs one launch: the norm in
  * its prologue and one activation quantization shared by all matrices (as
  * gemv_q4_pair shares one, crates/llm-cpu/src/gemv_q4.rs:396-443); otherwise
- * rms_norm then one lgh_q4_gemm per matrix.  Results equal that sequence. */
+ * rms_norm then one lgh_q4_gemm per matrix (for 5 or more tokens the norm is
+ * applied inside the shared activation-image kernel, from per-row scales).
+ * Results equal that sequence. */
 int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,
                      const float *hidden, float *const *y, size_t tokens, int mode);
 int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w_dev, float eps,

@@ -682,7 +682,20 @@ static int check_mode(lgh_ctx *ctx, int mode) {
   return LGH_OK;
 }
 
-static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
+// The activation rows a GEMM call quantizes: x itself, rms_norm(x, nw, eps)
+// (nw not null) or silu(x) * u (u not null).  Routes whose activation image
+// has a fused form build it from x directly; the others first write the rows
+// to tmp ([m][k] f32; for silu tmp is x itself, overwritten in place as the
+// op sequence's silu_mul does).
+struct ActIn {
+  const float *x;
+  const float *nw = nullptr;
+  float eps = 0.0f;
+  const float *u = nullptr;
+  float *tmp = nullptr;
+};
+
+static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, ActIn in,
                           float *const *y_dev, size_t m, int mode);
 static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
                        const int8_t *codes_dev, const float *scales_dev, float *const *y_dev, size_t m, int mode);
@@ -691,8 +704,8 @@ static int launch_gemv(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *w0, float *y0,
                        const float *x, int mode) {
   if (!lgh::plan_q4_gemv(w0->n, w0->bpr, w1 ? 2 : 1).ok) {
     // K longer than the GEMV covers: batched act-quant + GEMM with m = 1.
-    if (int r = gemm_multi_dev(ctx, wsp, &w0, 1, x, &y0, 1, mode)) return r;
-    return w1 ? gemm_multi_dev(ctx, wsp, &w1, 1, x, &y1, 1, mode) : LGH_OK;
+    if (int r = gemm_multi_dev(ctx, wsp, &w0, 1, ActIn{x}, &y0, 1, mode)) return r;
+    return w1 ? gemm_multi_dev(ctx, wsp, &w1, 1, ActIn{x}, &y1, 1, mode) : LGH_OK;
   }
   if (int r = set_device(ctx)) return r;
   if (lgh::q4_gemv_quantize_once(w0->n, w0->bpr, w1 ? 2 : 1)) {
@@ -837,7 +850,7 @@ static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int 
     Carve cv;
     l.o_ci = cv.take(mt * pq * 2 * 1024);
     l.o_si = cv.take(mt * pq * 256);
-    l.o_rs = cv.take(c * sizeof(float));
+    l.o_rs = cv.take(2 * c * sizeof(float));
     l.bytes = cv.off;
     return l;
   };
@@ -856,7 +869,7 @@ static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int 
     if (codes_dev)
       LGH_HIP(ctx, lgh::launch_act_codes_mma(codes_dev + m0 * k, scales_dev + m0 * bpr, mc, k, ci, si, ctx->stream));
     else
-      LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev + m0 * k, mc, k, ctx->act_mode, ci, si,
+      LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev + m0 * k, lgh::ActPrologue{}, mc, k, ctx->act_mode, ci, si,
                                              reinterpret_cast<float *>(ws + lay.o_rs), ctx->stream));
     for (int j = 0; j < nmat; j++)
       if (w[j]->n)
@@ -865,18 +878,44 @@ static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int 
   return LGH_OK;
 }
 
+// Write the transformed activation rows of `in` to in.tmp (rms_norm or silu * u,
+// the op sequence's kernels) and return them; plain rows are returned as they are.
+static int materialize(lgh_ctx *ctx, const ActIn &in, size_t m, size_t k, const float **rows) {
+  *rows = in.x;
+  if (!in.nw && !in.u) return LGH_OK;
+  if (!in.tmp || (in.u && in.tmp != in.x))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "no buffer for the transformed activation rows");
+  if (in.nw)
+    LGH_HIP(ctx, lgh::launch_rms_norm(in.x, in.nw, k, m, in.eps, in.tmp, ctx->stream));
+  else
+    LGH_HIP(ctx, lgh::launch_silu_mul(in.tmp, in.u, m * k, ctx->stream));
+  *rows = in.tmp;
+  return LGH_OK;
+}
+
 // y[j] = x @ W[j]^T for 1..3 matrices with the same k, m rows of x: the
 // activation quantization of each route (the MMA image, the GEMM's operand
 // image) is done once and read by every matrix.  m == 1 and m <= 4 quantize
-// inside their kernels, per matrix.
-static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, const float *x_dev,
+// inside their kernels, per matrix.  The rows may be rms_norm(x) or
+// silu(x) * u (ActIn): the MMA and GEMM routes form them inside their image
+// kernels (the norm from row scales computed first, without writing the normed
+// rows), the others after one more launch that writes them out.
+static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, ActIn in,
                           float *const *y_dev, size_t m, int mode) {
   const size_t k = w[0]->k, bpr = w[0]->bpr;
   size_t nmax = 0;
   for (int j = 0; j < nmat; j++) nmax = std::max(nmax, w[j]->n);
   if (m == 0 || nmax == 0) return LGH_OK;
-  if (!aligned16(x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  if (!aligned16(in.x) || !aligned16(in.u) || !aligned16(in.nw))
+    return fail(ctx, LGH_ERR_INVALID_ARG, "activation rows must be 16-byte aligned");
+  // The image kernels' elementwise step: silu(x) * u, or rms_norm (row scales first).
+  lgh::ActPrologue pro;
+  pro.u = in.nw ? nullptr : in.u;
+  pro.nw = in.nw;
+  pro.eps = in.eps;
+  const float *x_dev = in.x;
   if (m == 1 && lgh::plan_q4_gemv(nmax, bpr, 1).ok) {
+    if (int r = materialize(ctx, in, m, k, &x_dev)) return r;
     for (int j = 0; j < nmat; j++)
       if (w[j]->n)
         if (int r = launch_gemv(ctx, wsp, w[j], y_dev[j], nullptr, nullptr, x_dev, mode)) return r;
@@ -885,6 +924,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
   if (int r = set_device(ctx)) return r;
   // Small batches are weight-stream bound: nibble planes, no operand image.
   if (lgh::plan_q4_batch(m, bpr).ok) {  // m <= 4: dot4 on the nibble planes
+    if (int r = materialize(ctx, in, m, k, &x_dev)) return r;
     if (lgh::q4_batch_quantize_once(bpr)) {  // long rows: x quantized once, shared by every matrix
       Carve cv;
       const size_t oq = cv.take(m * k), os = cv.take(m * bpr * sizeof(float)), orow = cv.take(m * sizeof(float));
@@ -907,19 +947,22 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     const size_t mt = (m + 15) / 16, pq = (bpr + 3) / 4;
     Carve cv;
     const size_t o_ci = cv.take(mt * pq * 2 * 1024), o_si = cv.take(mt * pq * 256);
-    const size_t o_rs = cv.take(m * sizeof(float));
+    const size_t o_rs = cv.take(2 * m * sizeof(float));
     char *ws = nullptr;
     if (int r = wsp.get(cv.off, &ws)) return r;
     auto *ci = reinterpret_cast<uint8_t *>(ws + o_ci);
     auto *si = reinterpret_cast<float *>(ws + o_si);
-    LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev, m, k, ctx->act_mode, ci, si,
+    LGH_HIP(ctx, lgh::launch_act_quant_mma(x_dev, pro, m, k, ctx->act_mode, ci, si,
                                            reinterpret_cast<float *>(ws + o_rs), ctx->stream));
     for (int j = 0; j < nmat; j++)
       if (w[j]->n) LGH_HIP(ctx, lgh::launch_q4_gemv_mma(w[j], ci, si, y_dev[j], m, mode, ctx->stream));
     return LGH_OK;
   }
   for (int j = 0; j < nmat; j++)
-    if (w[j]->n && !mx_fits(w[j])) return mma_chunked(ctx, wsp, w, nmat, x_dev, nullptr, nullptr, y_dev, m, mode);
+    if (w[j]->n && !mx_fits(w[j])) {
+      if (int r = materialize(ctx, in, m, k, &x_dev)) return r;
+      return mma_chunked(ctx, wsp, w, nmat, x_dev, nullptr, nullptr, y_dev, m, mode);
+    }
   for (int j = 0; j < nmat; j++) {
     if (!w[j]->n) continue;
     if (wsp.fixed) {  // building the image allocates
@@ -954,7 +997,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     l.part_floats = splits > 1 ? static_cast<size_t>(splits) * c * rows : 0;
     Carve cv;
     l.o_mx = cv.take((c + 31) / 32 * rec_per_tile);
-    l.o_rs = cv.take(c * sizeof(float));
+    l.o_rs = cv.take(2 * c * sizeof(float));
     l.o_part = cv.take(l.part_floats * sizeof(float));
     l.bytes = cv.off;
     return l;
@@ -975,7 +1018,9 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     const size_t mc = std::min(chunk, m - m0);
     float *yc[3] = {nullptr, nullptr, nullptr};
     for (int j = 0; j < nmat; j++) yc[j] = w[j]->n ? y_dev[j] + m0 * w[j]->n : nullptr;
-    LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * k, mc, k, ctx->act_mode, mxa, rs, ctx->stream));
+    lgh::ActPrologue pc = pro;
+    if (pc.u) pc.u += m0 * k;
+    LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * k, pc, mc, k, ctx->act_mode, mxa, rs, ctx->stream));
     LGH_HIP(ctx, lgh::launch_q4_gemm(w, nmat, mxa, yc, mc, mode, splits, part, part_floats, ctx->stream));
   }
   return LGH_OK;
@@ -987,7 +1032,7 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
   if (int r = check_mode(ctx, mode)) return r;
   if (m == 0 || w->n == 0) return LGH_OK;
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
-  return gemm_multi_dev(ctx, grow_ws(ctx), &w, 1, x_dev, &y_dev, m, mode);
+  return gemm_multi_dev(ctx, grow_ws(ctx), &w, 1, ActIn{x_dev}, &y_dev, m, mode);
 }
 
 // lgh_q4_gemm_dev with every scratch buffer taken from the device's fixed
@@ -1004,7 +1049,7 @@ int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, f
   if (!y_dev || (w->k && !x_dev)) return fail(ctx, LGH_ERR_INVALID_ARG, "null x/y");
   if (!ctx->scratch) return fail(ctx, LGH_ERR_INVALID_ARG, "device %d has no fixed scratch", ctx->device);
   const Ws fixed{ctx, static_cast<char *>(ctx->scratch), LGH_NOALLOC_SCRATCH_BYTES};
-  return gemm_multi_dev(ctx, fixed, &w, 1, x_dev, &y_dev, m, mode);
+  return gemm_multi_dev(ctx, fixed, &w, 1, ActIn{x_dev}, &y_dev, m, mode);
 }
 
 // ---- measurement probes ------------------------------------------------------------
@@ -1246,21 +1291,21 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
   if (int r = set_device(ctx)) return r;
   if (tokens == 1 && lgh::ffn_gate_up_supported(w1)) return ffn_fused(ctx, w1, w3, w2, norm_w_dev, eps, hidden_dev);
   // Several tokens (or a wide model): the reference's sequence of ops
-  // (lfm2.rs:861-881), each on the device, intermediates in the context.
+  // (lfm2.rs:861-881) on the device, intermediates in the context.  The norm
+  // and silu(g) * u are formed inside the activation-image kernels of the
+  // gate/up and down GEMMs where those have a fused form (gemm_multi_dev).
   const size_t dim = w1->k, inter = w1->n;
   Carve cv;
   const size_t o_n = cv.take(norm_w_dev ? tokens * dim * sizeof(float) : 0);
   const size_t o_g = cv.take(tokens * inter * sizeof(float)), o_u = cv.take(tokens * inter * sizeof(float));
   if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, cv.off)) return r;
   char *f = static_cast<char *>(ctx->ffn);
-  float *normed = norm_w_dev ? reinterpret_cast<float *>(f + o_n) : hidden_dev;
   float *g = reinterpret_cast<float *>(f + o_g), *u = reinterpret_cast<float *>(f + o_u);
-  if (norm_w_dev) LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, dim, tokens, eps, normed, ctx->stream));
+  const ActIn normed{hidden_dev, norm_w_dev, eps, nullptr, norm_w_dev ? reinterpret_cast<float *>(f + o_n) : nullptr};
   const lgh_q4 *gate_up[2] = {w1, w3};
   float *gu[2] = {g, u};
   if (int r = gemm_multi_dev(ctx, grow_ws(ctx), gate_up, 2, normed, gu, tokens, LGH_ASSIGN)) return r;
-  LGH_HIP(ctx, lgh::launch_silu_mul(g, u, tokens * inter, ctx->stream));
-  return lgh_q4_gemm_dev(ctx, w2, g, hidden_dev, tokens, LGH_ADD_F64);
+  return gemm_multi_dev(ctx, grow_ws(ctx), &w2, 1, ActIn{g, nullptr, 0.0f, u, g}, &hidden_dev, tokens, LGH_ADD_F64);
 }
 
 int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2, const float *norm_w,
@@ -1353,15 +1398,14 @@ int lgh_q4_norm_gemv_dev(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, cons
     return LGH_OK;
   }
   // Otherwise the reference's sequence (rms_norm, then one apply per matrix;
-  // the matrices share each route's activation quantization).
-  const float *normed = hidden_dev;
+  // the matrices share each route's activation quantization, whose image
+  // kernel forms the norm where it has a fused form).
+  ActIn in{hidden_dev};
   if (norm_w_dev && k) {
     if (int r = ensure(ctx, &ctx->ffn, &ctx->ffn_bytes, tokens * k * sizeof(float))) return r;
-    float *nd = static_cast<float *>(ctx->ffn);
-    LGH_HIP(ctx, lgh::launch_rms_norm(hidden_dev, norm_w_dev, k, tokens, eps, nd, ctx->stream));
-    normed = nd;
+    in = ActIn{hidden_dev, norm_w_dev, eps, nullptr, static_cast<float *>(ctx->ffn)};
   }
-  return gemm_multi_dev(ctx, grow_ws(ctx), w, nm, normed, y_dev, tokens, mode);
+  return gemm_multi_dev(ctx, grow_ws(ctx), w, nm, in, y_dev, tokens, mode);
 }
 
 int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,

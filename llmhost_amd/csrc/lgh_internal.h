@@ -94,10 +94,23 @@ constexpr uint32_t kImageLayout = (1u << 16) | static_cast<uint32_t>(kMxWRec);
 
 // Weight operand image from the repacked nibble/scale planes (load time).
 hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t stream);
-// Activation operand image: quantize x[m][k] per ActQ8 (per_row selects the
-// mode; row_scale is scratch for m floats) straight into mt*pp records.
-hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, uint8_t *mxa,
-                               float *row_scale, hipStream_t stream);
+// The elementwise step an activation image kernel applies to x before ActQ8:
+// none, h = silu(x) * u (u [m][k]: the FFN's down-projection input, formed in
+// place of the silu_mul launch) or rms_norm(x, nw, eps) (nw [k], ops.rs:8-23:
+// nw * (x * scale_t) with the row scales from a one-wave-per-row kernel, in
+// place of rms_norm writing the normed rows).  Either way the image equals
+// the op sequence's bit for bit.  nscale is set by the launchers.
+struct ActPrologue {
+  const float *u = nullptr;
+  const float *nw = nullptr;
+  float eps = 0.0f;
+  const float *nscale = nullptr;
+};
+// Activation operand image: quantize the rows of x[m][k] (after the prologue)
+// per ActQ8 (per_row selects the mode) straight into mt*pp records.  scratch:
+// 2*m floats (row scales).
+hipError_t launch_act_quant_mx(const float *x, ActPrologue pro, size_t m, size_t k, int per_row, uint8_t *mxa,
+                               float *scratch, hipStream_t stream);
 // Same record layout from already-quantized int8 activations aq [m][k] and
 // their block scales [m][k/32] (scales null: 0).
 hipError_t launch_act_split_mx(const int8_t *aq, const float *scales, size_t m, size_t k, uint8_t *mxa,
@@ -192,8 +205,8 @@ struct Q4MmaPlan {
 // any_shape: a plan for every 1 <= m <= 64 and row length, also where the
 // route table prefers the GEMM (for matrices that cannot hold a GEMM image).
 Q4MmaPlan plan_q4_mma(size_t n, size_t m, size_t bpr, bool any_shape = false);
-hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row, uint8_t *codes, float *scales,
-                                float *row_scale, hipStream_t stream);
+hipError_t launch_act_quant_mma(const float *x, ActPrologue pro, size_t m, size_t k, int per_row, uint8_t *codes,
+                                float *scales, float *scratch, hipStream_t stream);
 // The same image from ActQ8 codes [m][k] and block scales [m][k/32].
 hipError_t launch_act_codes_mma(const int8_t *aq, const float *as, size_t m, size_t k, uint8_t *codes,
                                 float *scales, hipStream_t stream);

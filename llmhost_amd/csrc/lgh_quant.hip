@@ -17,13 +17,35 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
 // ---- batched activation quantization (gemv_q4.rs:747-798) -----------------
-__global__ __launch_bounds__(kThreads) void row_amax_kernel(const float *__restrict__ x, int k,
-                                                            float *row_scale) {
+// h = silu(g) * u elementwise on a float4 (the op sequence's silu_mul_kernel
+// arithmetic, so an image built from g and u equals one built from h).
+__device__ __forceinline__ float4 silu_mul4(float4 g, float4 u) {
+  return make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
+}
+
+// The elementwise prologue of an image kernel on float4 f of x (float4 fr of
+// token t's row): h = silu(x) * u, or the rms_norm output nw * (x * scale_t)
+// with the row's scale from row_norm_kernel; uniform branches.
+__device__ __forceinline__ void apply_prologue(const ActPrologue &pro, int t, size_t fr, size_t f, float4 &v) {
+  if (pro.u) {
+    v = silu_mul4(v, reinterpret_cast<const float4 *>(pro.u)[f]);
+  } else if (pro.nw) {
+    const float s = pro.nscale[t];
+    const float4 w = reinterpret_cast<const float4 *>(pro.nw)[fr];
+    v = make_float4(w.x * (v.x * s), w.y * (v.y * s), w.z * (v.z * s), w.w * (v.w * s));
+  }
+}
+
+// Row amax / 127 of x, or (u not null) of silu(x) * u.
+__global__ __launch_bounds__(kThreads) void row_amax_kernel(const float *__restrict__ x, const float *__restrict__ u,
+                                                            int k, float *row_scale) {
   __shared__ float s_red[kWaves];
   const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<size_t>(blockIdx.x) * k);
+  const float4 *u4 = u ? reinterpret_cast<const float4 *>(u + static_cast<size_t>(blockIdx.x) * k) : nullptr;
   float m = 0.0f;
   for (int i = threadIdx.x; i < k / 4; i += kThreads) {
     float4 v = x4[i];
+    if (u4) v = silu_mul4(v, u4[i]);
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   }
   m = wave_max(m);
@@ -276,8 +298,8 @@ __constant__ HlTable kHlTable = make_hl_table();
 // for bit; kernel trace): M=512, K=10752 7.96 -> 7.44 us, M=2048, K=10752
 // 25.0 -> 19.7 us, M=512, K=2048 unchanged (5.2 us); whole GEMM calls
 // 1.3-3.8% faster (interleaved A/B).
-__global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, int m, int bpr,
-                                                                int pp, int per_row, const float *row_scale,
+__global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__restrict__ x, ActPrologue pro, int m,
+                                                                int bpr, int pp, int per_row, const float *row_scale,
                                                                 uint32_t recs, uint8_t *mxa) {
   __shared__ uint16_t s_hl[256];
   __shared__ __align__(16) uint8_t s_rec[kMxARec];
@@ -289,9 +311,12 @@ __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__r
   const bool ok = r < recs && t < m && blk < bpr;
   float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
   if (ok) {
-    const float4 *src = reinterpret_cast<const float4 *>(x) + (static_cast<size_t>(t) * bpr + blk) * 8 + 2 * g;
+    const size_t f = (static_cast<size_t>(t) * bpr + blk) * 8 + 2 * g;
+    const float4 *src = reinterpret_cast<const float4 *>(x) + f;
     a = src[0];
     b = src[1];
+    apply_prologue(pro, t, blk * 8 + 2 * g, f, a);
+    apply_prologue(pro, t, blk * 8 + 2 * g + 1, f + 1, b);
   }
   s_hl[tid] = kHlTable.v[tid];
   __syncthreads();  // the table
@@ -361,8 +386,8 @@ __global__ __launch_bounds__(kThreads) void act_split_mx_kernel(const int8_t *__
 // Activations for the matrix-core batch GEMV, in its MFMA register layouts
 // (lgh_internal.h): one 8-lane group per (token, block) over the padded
 // ranges [0, 16*mt) x [0, 4*pq); padding gets code 0 and scale 0.
-__global__ __launch_bounds__(kThreads) void act_quant_mma_kernel(const float *__restrict__ x, int m, int bpr,
-                                                                 int pq, int per_row, const float *row_scale,
+__global__ __launch_bounds__(kThreads) void act_quant_mma_kernel(const float *__restrict__ x, ActPrologue pro, int m,
+                                                                 int bpr, int pq, int per_row, const float *row_scale,
                                                                  size_t groups, uint8_t *codes, float *scales) {
   const size_t gi = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
   if (gi >= groups) return;  // whole 8-lane groups exit together
@@ -370,7 +395,11 @@ __global__ __launch_bounds__(kThreads) void act_quant_mma_kernel(const float *__
   const int t = static_cast<int>(gi / (4 * pq)), b = static_cast<int>(gi % (4 * pq));
   const bool ok = t < m && b < bpr;
   float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (ok) v = reinterpret_cast<const float4 *>(x)[(static_cast<size_t>(t) * bpr + b) * 8 + g8];
+  if (ok) {
+    const size_t f = (static_cast<size_t>(t) * bpr + b) * 8 + g8;
+    v = reinterpret_cast<const float4 *>(x)[f];
+    apply_prologue(pro, t, b * 8 + g8, f, v);
+  }
   const bool pr = ok && per_row;
   const float rs = pr ? row_scale[t] : 0.0f;
   float scale;
@@ -403,6 +432,73 @@ __global__ __launch_bounds__(kThreads) void act_codes_mma_kernel(const int8_t *_
   if (g8 == 0) scales[((static_cast<size_t>(t >> 4) * pq + (b >> 2)) * 16 + (t & 15)) * 4 + (b & 3)] = ok ? as[blk] : 0.0f;
 }
 
+// ---- rms_norm scales for the activation images --------------------------------
+// The row's sum of squares in exactly rms_norm_kernel's order (256 threads:
+// thread i adds the f64 squares of elements i, i + 256, ... in turn, each
+// wave's 64 partials meet in wave_sum_dpp64's tree, the 4 wave sums are added
+// in order), so the scale -- and every normed value nw * (x * scale) -- equals
+// the op sequence's bit for bit.  Element 4 lane + c + 256 j sits in component
+// c of the lane's float4 lane + 64 j, i.e. belongs to thread 4 lane + c: the
+// lane keeps those 4 partials (j in order), and thread 64 v + L's partial is
+// fetched into lane L to replay wave v's tree.
+__device__ __forceinline__ double replay_256_thread_sum(double p0, double p1, double p2, double p3) {
+  const int lane = threadIdx.x & (kWave - 1), sel = lane & 3;
+  double tot = 0.0;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int src = 16 * v + (lane >> 2);
+    const double t0 = __shfl(p0, src, kWave), t1 = __shfl(p1, src, kWave);
+    const double t2 = __shfl(p2, src, kWave), t3 = __shfl(p3, src, kWave);
+    const double mine = sel == 0 ? t0 : sel == 1 ? t1 : sel == 2 ? t2 : t3;
+    tot += wave_sum_dpp64(mine);
+  }
+  return tot;
+}
+
+constexpr int kRnBatch = 8;  // float4s per lane in flight
+
+// One wave per token row (4 per workgroup): nscale[t] = the rms_norm scale of
+// row t (ops.rs:12-17) and, with row_scale, the PerRow scale of the normed row
+// (amax(nw * (x * scale)) / 127, as row_amax_kernel over rms_norm's output).
+// The image kernels then quantize nw * (x * nscale[t]) element by element.
+__global__ __launch_bounds__(kThreads) void row_norm_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                            double inv_k, float eps, int m, int bpr, float *nscale,
+                                                            float *row_scale) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x >> 6);
+  if (t >= m) return;  // whole waves
+  const uint32_t row_bytes = static_cast<uint32_t>(bpr) * 128u;
+  const auto xr = make_rsrc(x + static_cast<size_t>(t) * bpr * 32, row_bytes);
+  const int nj = (bpr * 8 + 63) / 64;  // float4s per lane (past the row: 0 through the range check)
+  double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
+  for (int j0 = 0; j0 < nj; j0 += kRnBatch) {
+    float4 v[kRnBatch];
+#pragma unroll
+    for (int i = 0; i < kRnBatch; i++) v[i] = buf_load_f4(xr, static_cast<uint32_t>(lane + 64 * (j0 + i)) * 16u);
+#pragma unroll
+    for (int i = 0; i < kRnBatch; i++) {  // squares past the row add +0.0 exactly
+      const double a = v[i].x, b = v[i].y, c = v[i].z, d = v[i].w;
+      p0 += a * a;
+      p1 += b * b;
+      p2 += c * c;
+      p3 += d * d;
+    }
+  }
+  const float scale = rms_scale(replay_256_thread_sum(p0, p1, p2, p3), inv_k, eps);
+  if (lane == 0) nscale[t] = scale;
+  if (!row_scale) return;  // uniform
+  const auto nr = make_rsrc(nw, row_bytes);
+  float mx = 0.0f;
+  for (int j = 0; j < nj; j++) {
+    const uint32_t off = static_cast<uint32_t>(lane + 64 * j) * 16u;
+    const float4 a = buf_load_f4(xr, off), w = buf_load_f4(nr, off);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w.x * (a.x * scale)), fabsf(w.y * (a.y * scale))),
+                         fmaxf(fabsf(w.z * (a.z * scale)), fabsf(w.w * (a.w * scale)))));
+  }
+  mx = wave_max(mx);
+  if (lane == 0) row_scale[t] = div127_rn(mx);
+}
+
 inline unsigned blocks_for(size_t items, unsigned per) {
   return static_cast<unsigned>((items + per - 1) / per);
 }
@@ -418,37 +514,49 @@ hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_act_quant_mx(const float *x, size_t m, size_t k, int per_row, uint8_t *mxa, float *row_scale,
-                               hipStream_t st) {
+// The row statistics an image kernel needs before it starts: the PerRow scale
+// (row_amax_kernel over x or silu(x) * u) or, for the norm, the rms_norm
+// scales and the PerRow scale of the normed rows (row_norm_kernel).
+// scratch: 2 * m floats; on return pro.nscale is set for the norm.
+hipError_t row_stats(const float *x, ActPrologue &pro, size_t m, size_t k, int per_row, float *scratch,
+                     const float **row_scale, hipStream_t st) {
+  *row_scale = per_row ? scratch : nullptr;
+  if (pro.nw) {
+    pro.nscale = scratch + m;
+    hipLaunchKernelGGL(row_norm_kernel, dim3(static_cast<unsigned>((m + kWaves - 1) / kWaves)), dim3(kThreads), 0, st,
+                       x, pro.nw, 1.0 / static_cast<double>(k), pro.eps, static_cast<int>(m),
+                       static_cast<int>(k / 32), scratch + m, per_row ? scratch : nullptr);
+    return hipGetLastError();
+  }
+  if (!per_row) return hipSuccess;
+  hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x, pro.u,
+                     static_cast<int>(k), scratch);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_mx(const float *x, ActPrologue pro, size_t m, size_t k, int per_row, uint8_t *mxa,
+                               float *scratch, hipStream_t st) {
   const size_t bpr = k / 32, pp = (bpr + 1) / 2, mt = (m + 31) / 32;
   if (m == 0 || bpr == 0) return hipSuccess;
-  if (per_row) {
-    hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x,
-                       static_cast<int>(k), row_scale);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  const float *rs = nullptr;
+  if (hipError_t e = row_stats(x, pro, m, k, per_row, scratch, &rs, st)) return e;
   const size_t recs = mt * pp;  // < 2^31: the image is below kMxMaxBytes
-  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(static_cast<unsigned>(recs)), dim3(kThreads), 0, st, x,
-                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), per_row, row_scale,
+  hipLaunchKernelGGL(act_quant_mx_kernel, dim3(static_cast<unsigned>(recs)), dim3(kThreads), 0, st, x, pro,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pp), per_row, rs,
                      static_cast<uint32_t>(recs), mxa);
   return hipGetLastError();
 }
 
-hipError_t launch_act_quant_mma(const float *x, size_t m, size_t k, int per_row, uint8_t *codes, float *scales,
-                                float *row_scale, hipStream_t st) {
+hipError_t launch_act_quant_mma(const float *x, ActPrologue pro, size_t m, size_t k, int per_row, uint8_t *codes,
+                                float *scales, float *scratch, hipStream_t st) {
   const size_t bpr = k / 32, pq = (bpr + 3) / 4, mt = (m + 15) / 16;
   if (m == 0 || bpr == 0) return hipSuccess;
-  if (per_row) {
-    hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x,
-                       static_cast<int>(k), row_scale);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  const float *rs = nullptr;
+  if (hipError_t e = row_stats(x, pro, m, k, per_row, scratch, &rs, st)) return e;
   const size_t groups = mt * 16 * pq * 4;
-  hipLaunchKernelGGL(act_quant_mma_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x,
-                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pq), per_row, row_scale, groups,
-                     codes, scales);
+  hipLaunchKernelGGL(act_quant_mma_kernel, dim3(blocks_for(groups * 8, kThreads)), dim3(kThreads), 0, st, x, pro,
+                     static_cast<int>(m), static_cast<int>(bpr), static_cast<int>(pq), per_row, rs, groups, codes,
+                     scales);
   return hipGetLastError();
 }
 
@@ -525,7 +633,7 @@ hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int
   if (m == 0 || k == 0) return hipSuccess;
   const size_t bpr = k / 32;
   if (per_row) {
-    hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x,
+    hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x, nullptr,
                        static_cast<int>(k), row_scale);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

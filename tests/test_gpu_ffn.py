@@ -247,3 +247,47 @@ def test_ffn_residual_tokens_device_path(gpu_ctx, oracle):
     q4.ffn_residual(*gpu, torch.from_numpy(nw).cuda(), 1e-5, dev, tokens=t)
     torch.cuda.synchronize()
     assert np.array_equal(dev.cpu().numpy(), host)
+
+
+# (dim, inter, tokens): the matrix-core batch route (5-64 tokens) and the GEMM route (65+), rows
+# of an odd block count (1568 = 49 blocks: a padding block in every pair), token counts that end
+# inside a 16- and a 32-token tile, the down GEMM with split K (inter 4096, 130 tokens), and rows
+# longer than the fused norm covers (2080 = 65 blocks: rms_norm is written out first).
+PREFILL = [(1536, 2048, 5), (1568, 2048, 37), (1536, 4096, 130), (1568, 1024, 100), (2048, 1536, 513),
+           (2080, 512, 70), (96, 64, 65), (1536, 8192, 64)]
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("dim,inter,t", PREFILL)
+def test_prefill_fusions_equal_op_sequence(gpu_ctx, oracle, dim, inter, t, per_row):
+    """The prefill FFN block forms rms_norm(hidden) inside the gate/up activation image and
+    silu(g) * u inside the down projection's image: bit for bit the op sequence it replaces
+    (rms_norm; the gate/up pair on one shared activation quantization; silu_mul; the down GEMM
+    added in f64), in both act-quant modes.  The same for the norm + projections entry point."""
+    print(f"[prefill fusion] dim={dim} inter={inter} t={t} per_row={per_row}", flush=True)
+    gpu, _ = _mats(gpu_ctx, oracle, dim, inter, 300 + dim + t)
+    hidden = (synth.activations(310 + t, t, dim) * np.float32(2.0)).astype(np.float32).ravel()
+    nw = (1 + 0.2 * synth.normal_f32(311 + dim, dim)).astype(np.float32)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        fused = hidden.copy()
+        q4.ffn_residual(*gpu, nw, 1e-5, fused, tokens=t)
+        normed = np.zeros_like(hidden)
+        q4.rms_norm(hidden, nw, 1e-5, normed, gpu_ctx)
+        g = np.zeros(t * inter, np.float32)
+        u = np.zeros(t * inter, np.float32)
+        q4.norm_gemv(gpu[:2], None, 1e-5, normed, [g, u], t)
+        q4.silu_mul(g, u, gpu_ctx)
+        seq = hidden.copy()
+        q4.gemm_q4_add(gpu[2], g, seq, t)
+        # norm + projections: fused vs rms_norm then the same launch without the norm
+        gu_fused = [np.zeros(t * inter, np.float32), np.zeros(t * inter, np.float32)]
+        q4.norm_gemv(gpu[:2], nw, 1e-5, hidden, gu_fused, t)
+        g2, u2 = np.zeros(t * inter, np.float32), np.zeros(t * inter, np.float32)
+        q4.norm_gemv(gpu[:2], None, 1e-5, normed, [g2, u2], t)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+    assert np.isfinite(fused).all()
+    assert fused.tobytes() == seq.tobytes(), "FFN block differs from the op sequence"
+    assert gu_fused[0].tobytes() == g2.tobytes() and gu_fused[1].tobytes() == u2.tobytes(), \
+        "norm + projections differ from rms_norm then the projections"
