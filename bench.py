@@ -648,46 +648,59 @@ def cpu_baseline(target_s: float = 10.0, row_s: float = 4.0):
             "ms_per_step": round(el / calls * 1e3, 4), "host": host, "rows": rows}
 
 
-def counters_mode(iters: int = 50) -> None:
-    """Eager launches for hardware-counter runs (rocprofv3 --pmc): `iters`
-    launches of each headline GEMV over rotating copies, 5 prefill GEMMs
-    (M=512, K=2048, N=10752), then a plain 64 MiB device-to-device copy
-    (torch) of known size to calibrate FETCH_SIZE / WRITE_SIZE against.
-    Prints the byte counts each kernel should move."""
+COUNTER_CASES = ("gemv", "gemm_m512_k2048", "gemm_m512_k10752", "ragged_m64", "copy")
+
+
+def counters_mode(cases=COUNTER_CASES, iters: int = 50) -> None:
+    """Eager launches for hardware-counter runs (rocprofv3 --pmc), one group per case:
+    gemv: `iters` launches of each headline GEMV over rotating copies; gemm_m512_k2048 /
+    gemm_m512_k10752: 5 prefill GEMM calls (M=512; K=2048, N=10752 / K=10752, N=2048);
+    ragged_m64: 20 calls of the ragged M=64, K=2048, N=8192 GEMM; copy: a plain 64 MiB
+    device-to-device copy (torch) of known size to calibrate FETCH_SIZE / WRITE_SIZE against.
+    Prints the byte / op counts each kernel should move."""
     gb = GpuBench()
     torch, q4 = gb.torch, gb.q4
     from llmhost_amd import synth
 
-    for i, (name, n, k) in enumerate([("up", 8192, 1536), ("down", 1536, 8192)]):
-        _, mats = gb.copies(n, k, 101 + i, 2 * MALL_BYTES + (64 << 20))
-        x = torch.from_numpy(synth.normal_f32(201 + i, k)).cuda()
-        y = torch.zeros(n, device="cuda")
+    if "gemv" in cases:
+        for i, (name, n, k) in enumerate([("up", 8192, 1536), ("down", 1536, 8192)]):
+            _, mats = gb.copies(n, k, 101 + i, 2 * MALL_BYTES + (64 << 20))
+            x = torch.from_numpy(synth.normal_f32(201 + i, k)).cuda()
+            y = torch.zeros(n, device="cuda")
+            with torch.cuda.stream(gb.stream):
+                for it in range(iters):
+                    q4.gemv_q4(mats[it % len(mats)], x, y)
+            torch.cuda.synchronize()
+            log(f"[counters] {name}: {iters} launches, algorithmic bytes/launch {q4_bytes(n, k)} "
+                f"(weights {n * (k // 32) * 18})")
+            for w in mats:
+                w.free()
+    for case, (m, n, k, calls) in (("gemm_m512_k2048", (512, 10752, 2048, 5)),
+                                   ("gemm_m512_k10752", (512, 2048, 10752, 5)),
+                                   ("ragged_m64", (64, 8192, 2048, 20))):
+        if case not in cases:
+            continue
+        _, mats = gb.copies(n, k, 401 + k, 1)
+        if m > 64:
+            mats[0].prepare_gemm()
+        x = torch.from_numpy(synth.activations(402, m, k)).cuda()
+        y = torch.zeros(m, n, device="cuda")
         with torch.cuda.stream(gb.stream):
-            for it in range(iters):
-                q4.gemv_q4(mats[it % len(mats)], x, y)
+            for _ in range(calls):
+                q4.gemm_q4(mats[0], x, y, m)
         torch.cuda.synchronize()
-        log(f"[counters] {name}: {iters} launches, algorithmic bytes/launch {q4_bytes(n, k)} "
-            f"(weights {n * (k // 32) * 18})")
+        log(f"[counters] {case} M={m} K={k} N={n}: {calls} calls, {2 * m * n * k} int8 ops and "
+            f"{q4_bytes(n, k, m)} algorithmic bytes each")
         for w in mats:
             w.free()
-    m, n, k = 512, 10752, 2048
-    _, mats = gb.copies(n, k, 401, 1)
-    x = torch.from_numpy(synth.activations(402, m, k)).cuda()
-    y = torch.zeros(m, n, device="cuda")
-    with torch.cuda.stream(gb.stream):
-        for _ in range(5):
-            q4.gemm_q4(mats[0], x, y, m)
-    torch.cuda.synchronize()
-    log(f"[counters] gemm M={m} K={k} N={n}: 5 launches, {2 * m * n * k} int8 ops each")
-    for w in mats:
-        w.free()
-    src = torch.ones(16 << 20, device="cuda")
-    dst = torch.empty_like(src)
-    with torch.cuda.stream(gb.stream):
-        for _ in range(iters):
-            dst.copy_(src)
-    torch.cuda.synchronize()
-    log(f"[counters] copy: {iters} launches of a 64 MiB read + 64 MiB write")
+    if "copy" in cases:
+        src = torch.ones(16 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(gb.stream):
+            for _ in range(iters):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[counters] copy: {iters} launches of a 64 MiB read + 64 MiB write")
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_hbm_traffic.txt")
@@ -793,13 +806,22 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline GEMV only")
-    ap.add_argument("--counters", action="store_true",
-                    help="eager launches for rocprofv3 --pmc runs (no JSON line)")
+    ap.add_argument("--counters", nargs="?", const=",".join(COUNTER_CASES), default=None,
+                    help="eager launches for rocprofv3 --pmc runs (no JSON line); optionally a comma-separated "
+                         f"subset of {','.join(COUNTER_CASES)}")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated extra rows to run alone (no headline, no CPU baseline), e.g. for "
+                         "a per-shape kernel trace")
     ap.add_argument("--jsonl", default=None,
                     help="also append decode rows in the reference benchmark's JSONL schema to this file")
     args = ap.parse_args()
     if args.counters:
-        counters_mode()
+        cases = args.counters.split(",")
+        unknown = set(cases) - set(COUNTER_CASES)
+        if unknown:
+            print(f"bench.py --counters: unknown cases {sorted(unknown)}", file=sys.stderr)
+            sys.exit(2)
+        counters_mode(cases)
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the hot path is a "
@@ -807,7 +829,52 @@ def main():
               "built)", file=sys.stderr)
         sys.exit(2)
 
+    # Every `extra` row: (key, progress label, function; `gb` is bound below).  --only runs the
+    # named rows alone (for per-shape kernel traces and counters) and skips the headline.
+    sections = [("decode_sweep_16L", "decode sweep", lambda: decode_sweep(gb, 10))]
+    for m in (4, 16, 64):
+        sections.append((f"ragged_gemm_m{m}", f"ragged gemm M={m}", lambda m=m: gemm_case(gb, m, 8192, 2048, 50, 300 + m)))
+    for (m, n, k) in [(512, 10752, 2048), (512, 2048, 10752), (2048, 10752, 2048), (2048, 2048, 10752)]:
+        sections.append((f"prefill_gemm_m{m}_k{k}_n{n}", f"prefill gemm M={m} K={k} N={n}",
+                         lambda m=m, n=n, k=k: gemm_case(gb, m, n, k, 10, 400 + m + k)))
+    sections += [
+        ("q8_gemv_k1536_n1536", "q8 gemv", lambda: q8_case(gb, 200)),
+        ("q4_gemv_k1536_n1536", "Q4 GEMV K=N=1536 (the target's smallest shape)",
+         lambda: q4_head_case(gb, 200, 1536, 1536)),
+        ("q8_head_k1536_n65536", "tied head (N=65536, K=1536): Q8_0", lambda: q8_case(gb, 20, 65536, 1536)),
+        ("final_norm_q8_head_k1536_n65536", "final norm + Q8_0 head", lambda: q8_head_norm_case(gb, 20)),
+        ("decode_step_16L_chained", "chained 16-layer decode step (fused entry points)",
+         lambda: decode_step_case(gb, 10)),
+        ("q4_head_k1536_n65536", "tied head (N=65536, K=1536): Q4", lambda: q4_head_case(gb, 20)),
+        ("q4_gemv_size_sweep", "Q4 GEMV size sweep (launch floor -> HBM bound)", lambda: [
+            {k: round(v, 3) if isinstance(v, float) else v for k, v in q4_head_case(gb, 40, n, k).items()}
+            for (n, k) in ((8192, 1536), (16384, 1536), (32768, 1536), (65536, 1536), (131072, 1536),
+                           (1536, 8192), (4096, 8192), (16384, 8192))]),
+        ("ffn_block_dim1536_inter8192", "decode FFN block (fused vs per-op)", lambda: ffn_case(gb, 100)),
+        ("attn_qkv_dim1536", "attention block input side (norm + q/k/v, fused vs op sequence)",
+         lambda: block_input_case(gb, 100, (1536, 512, 512))),
+        ("conv_in_proj_dim1536", "conv block input side (norm + in_proj)", lambda: block_input_case(gb, 100, (4608,))),
+        ("attn_qkv_dim1536_prefill_m512", "attention block input side, 512 tokens",
+         lambda: block_input_case(gb, 10, (1536, 512, 512), tokens=512)),
+        ("ffn_block_dim1536_inter8192_prefill_m512",
+         "prefill FFN block (norm and silu * u fused into the activation images vs op sequence)",
+         lambda: ffn_prefill_case(gb, 10)),
+    ]
+    only = set(args.only.split(",")) if args.only else None
+    if only:
+        unknown = only - {key for key, _, _ in sections}
+        if unknown:
+            print(f"bench.py --only: unknown rows {sorted(unknown)}", file=sys.stderr)
+            sys.exit(2)
     gb = GpuBench()
+    if only:
+        extra = {}
+        for key, label, fn in sections:
+            if key in only:
+                log(f"[bench] {label}")
+                extra[key] = fn()
+        print(json.dumps({"metric": METRIC, "only": sorted(only), "extra": extra}), flush=True)
+        return
     log("[bench] headline GEMV workload")
     ms, step_bytes, copies, per_kernel, _ = gemv_workload(gb, args.steps, args.warmup)
     value = step_bytes / (ms * 1e-3) / 1e9
@@ -817,36 +884,9 @@ def main():
     log("[bench] launch floor and plain 7.1 MB read (same harness)")
     extra["launch_floor_and_read"] = launch_floor_and_read(gb, per_kernel)
     if not args.quick:
-        log("[bench] decode sweep")
-        extra["decode_sweep_16L"] = decode_sweep(gb, 10)
-        log("[bench] gemm cases")
-        for m in (4, 16, 64):
-            extra[f"ragged_gemm_m{m}"] = gemm_case(gb, m, 8192, 2048, 50, 300 + m)
-        for (m, n, k) in [(512, 10752, 2048), (512, 2048, 10752), (2048, 10752, 2048), (2048, 2048, 10752)]:
-            extra[f"prefill_gemm_m{m}_k{k}_n{n}"] = gemm_case(gb, m, n, k, 10, 400 + m + k)
-        log("[bench] q8 gemv")
-        extra["q8_gemv_k1536_n1536"] = q8_case(gb, 200)
-        log("[bench] Q4 GEMV K=N=1536 (the target's smallest shape)")
-        extra["q4_gemv_k1536_n1536"] = q4_head_case(gb, 200, 1536, 1536)
-        log("[bench] tied head (N=65536, K=1536): Q8_0 and Q4")
-        extra["q8_head_k1536_n65536"] = q8_case(gb, 20, 65536, 1536)
-        extra["final_norm_q8_head_k1536_n65536"] = q8_head_norm_case(gb, 20)
-        log("[bench] chained 16-layer decode step (fused entry points)")
-        extra["decode_step_16L_chained"] = decode_step_case(gb, 10)
-        extra["q4_head_k1536_n65536"] = q4_head_case(gb, 20)
-        log("[bench] Q4 GEMV size sweep (launch floor -> HBM bound)")
-        extra["q4_gemv_size_sweep"] = [
-            {k: round(v, 3) if isinstance(v, float) else v for k, v in q4_head_case(gb, 40, n, k).items()}
-            for (n, k) in ((8192, 1536), (16384, 1536), (32768, 1536), (65536, 1536), (131072, 1536),
-                           (1536, 8192), (4096, 8192), (16384, 8192))]
-        log("[bench] decode FFN block (fused vs per-op)")
-        extra["ffn_block_dim1536_inter8192"] = ffn_case(gb, 100)
-        log("[bench] attention / conv block input side (norm + projections, fused vs op sequence)")
-        extra["attn_qkv_dim1536"] = block_input_case(gb, 100, (1536, 512, 512))
-        extra["conv_in_proj_dim1536"] = block_input_case(gb, 100, (4608,))
-        extra["attn_qkv_dim1536_prefill_m512"] = block_input_case(gb, 10, (1536, 512, 512), tokens=512)
-        log("[bench] prefill FFN block (norm and silu * u fused into the activation images vs op sequence)")
-        extra["ffn_block_dim1536_inter8192_prefill_m512"] = ffn_prefill_case(gb, 10)
+        for key, label, fn in sections:
+            log(f"[bench] {label}")
+            extra[key] = fn()
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")
