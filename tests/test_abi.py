@@ -81,3 +81,23 @@ def test_cpp_header_compiles_and_matches_the_block_formats(tmp_path):
     inc = os.path.dirname(_ffi.HEADER_PATH)
     subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-I", inc, str(src)],
                    check=True)
+
+
+def test_rust_ffi_in_integration_doc_declares_every_export():
+    """INTEGRATION.md's src/ffi.rs block has one declaration per function of the C header, with the
+    same parameter count, so the Rust crate written from it binds the whole boundary."""
+    integ = open(os.path.join(os.path.dirname(_ffi.HEADER_PATH), "..", "INTEGRATION.md")).read()
+    start = integ.index('extern "C" {')
+    block = integ[start:integ.index("\n}\n", start)]
+    rust = {}
+    for name, params in re.findall(r"pub fn (lgh_\w+)\(([^)]*)\)", block, flags=re.S):
+        assert name not in rust, f"{name} declared twice"
+        rust[name] = 0 if not params.strip() else params.count(":")
+    text = re.sub(r"/\*.*?\*/", "", open(_ffi.HEADER_PATH).read(), flags=re.S)
+    header = {}
+    for name, params in re.findall(r"\b(lgh_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = params.strip()
+        header[name] = 0 if params in ("", "void") else params.count(",") + 1
+    assert set(rust) == set(header), (sorted(set(header) - set(rust)), sorted(set(rust) - set(header)))
+    for name, n in header.items():
+        assert rust[name] == n, f"{name}: {rust[name]} Rust parameters, {n} in the header"
