@@ -769,8 +769,8 @@ int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, co
     }
     if (int r = ensure_mx(ctx, w)) return r;
     const lgh_q4 *ws1[1] = {w};
-    const int splits = lgh::plan_q4_gemm_splits(ws1, 1, 1);
-    const size_t part_floats = splits > 1 ? static_cast<size_t>(splits) * w->n : 0;
+    const lgh::GemmPlan plan = lgh::plan_q4_gemm(ws1, 1, 1);
+    const size_t part_floats = plan.splits > 1 ? static_cast<size_t>(plan.splits) * w->n : 0;
     Carve cv;
     const size_t o_mx = cv.take(w->pp * lgh::kMxARec), o_part = cv.take(part_floats * sizeof(float));
     char *ws = nullptr;
@@ -778,7 +778,7 @@ int lgh_q4_gemv_prep_dev(lgh_ctx *ctx, const lgh_q4 *w, const int8_t *qs_dev, co
     auto *mxa = reinterpret_cast<uint8_t *>(ws + o_mx);
     LGH_HIP(ctx, lgh::launch_act_split_mx(qs_dev, scales_dev, 1, w->k, mxa, ctx->stream));
     float *ys[1] = {y_dev};
-    LGH_HIP(ctx, lgh::launch_q4_gemm(ws1, 1, mxa, ys, 1, mode, splits, reinterpret_cast<float *>(ws + o_part),
+    LGH_HIP(ctx, lgh::launch_q4_gemm(ws1, 1, mxa, ys, 1, mode, plan, reinterpret_cast<float *>(ws + o_part),
                                      part_floats, ctx->stream));
     return LGH_OK;
   }
@@ -983,12 +983,13 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
   if (cap_tiles <= 8) return fail(ctx, LGH_ERR_SHAPE, "K=%zu is too long for the GEMM path", k);
   size_t rows = 0;
   for (int j = 0; j < nmat; j++) rows += w[j]->n;
-  // The split count sets the order of the f32 additions, so it is planned
-  // once, for the token chunk the allocating path takes, and kept when the
-  // fixed scratch forces smaller chunks: chunking changes only the scratch
-  // footprint, never the result.
+  // The plan (K splits and K groups) sets the order of the f32 additions, so
+  // it is made once, for the token chunk the allocating path takes, and kept
+  // when the fixed scratch forces smaller chunks: chunking changes only the
+  // scratch footprint, never the result.
   const size_t chunk0 = std::min(m, (cap_tiles - 8) * 32);
-  const int splits = lgh::plan_q4_gemm_splits(w, nmat, chunk0);
+  const lgh::GemmPlan plan = lgh::plan_q4_gemm(w, nmat, chunk0);
+  const int splits = plan.splits;
   struct Layout {
     size_t part_floats, o_mx, o_rs, o_part, bytes;
   };
@@ -1021,7 +1022,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     lgh::ActPrologue pc = pro;
     if (pc.u) pc.u += m0 * k;
     LGH_HIP(ctx, lgh::launch_act_quant_mx(x_dev + m0 * k, pc, mc, k, ctx->act_mode, mxa, rs, ctx->stream));
-    LGH_HIP(ctx, lgh::launch_q4_gemm(w, nmat, mxa, yc, mc, mode, splits, part, part_floats, ctx->stream));
+    LGH_HIP(ctx, lgh::launch_q4_gemm(w, nmat, mxa, yc, mc, mode, plan, part, part_floats, ctx->stream));
   }
   return LGH_OK;
 }

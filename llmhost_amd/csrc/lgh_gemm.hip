@@ -39,6 +39,7 @@ constexpr long kSplitTarget = 512;  // two workgroups per CU (M=512, K=10752, N=
 constexpr size_t kSplitMinPairs = 64;  // K >= 4096
 constexpr size_t kSplitPairs = 16;     // K >= 1024 per split
 constexpr long kWideWgs = 640;  // 128 x 64 workgroup tiles from this many of them (2.5 per CU), no split K
+constexpr long kKgTiles = 512;  // two K groups per workgroup below this many 128 x 32 tiles (no split K)
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]
@@ -142,21 +143,27 @@ __device__ __forceinline__ uint32_t lds_addr(const char *p) {
 // hardware range check is only guaranteed on the VGPR offset, so every
 // address is kept inside the image by construction: record-0 offsets of
 // tiles past the image and of padding slots are >= 2^31 (out of range ->
-// zeros), and a stage p >= pend (prefetched past the end of the range, never
-// computed) re-reads stage pend - 1.
+// zeros), and a stage p >= plive (prefetched past the end of the range and
+// never computed, or a stage a K group runs only to keep its barriers in step
+// with the other group's) loads zeros: its loads go through a resource of
+// size 0 (every offset out of range) with soffset 0.  Either way the stage
+// issues its WPW loads, so the vmcnt waits keep counting stages, and the
+// VGPR offsets stay the loop-invariant ones.
 template <class C>
-__device__ __forceinline__ void dma_stage(const GemmArgs &g, const Slots<C> &s, int wave, int p, int pend,
+__device__ __forceinline__ void dma_stage(const GemmArgs &g, const Slots<C> &s, int wave, int p, int plive,
                                           const char *buf) {
   const i32x4 rw = sgpr_rsrc(g.wmx, g.w_bytes);
   const i32x4 ra = sgpr_rsrc(g.amx, g.a_bytes);
+  const i32x4 rz = sgpr_rsrc(g.wmx, 0u);
   const uint32_t base = lds_addr(buf);
-  const int q = uniform(min(p, pend - 1));
+  const bool live = p < plive;  // wave-uniform
+  const int q = uniform(live ? p : 0);
   const uint32_t sw = static_cast<uint32_t>(q * kWRec), sa = static_cast<uint32_t>(q * kARec);
 #pragma unroll
   for (int i = 0; i < C::WPW; i++) {
     const int j = wave + 4 * i;  // wave-uniform: the selects below are scalar
     const bool wt = j < C::WL_W;
-    dma16(wt ? rw : ra, s.off[i], wt ? sw : sa, base + 1024u * static_cast<uint32_t>(j));
+    dma16(live ? (wt ? rw : ra) : rz, s.off[i], wt ? sw : sa, base + 1024u * static_cast<uint32_t>(j));
   }
 }
 
@@ -293,26 +300,33 @@ __device__ __forceinline__ void wait_vm_barrier() {
 // flight; after the barrier every wave's DMAs of stage p are complete and
 // every wave is done reading `nxt`.
 template <class C, int TN, int TM, int NB>
-__device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int wave, int p, int pend,
+__device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> &slots, int wave, int p, int plive,
                                               const char *cur, char *nxt, const StageOffs &o,
                                               float (&acc)[TN][TM][16]) {
   wait_vm_barrier<(NB - 2) * C::WPW>();
-  dma_stage<C>(g, slots, wave, p + NB - 1, pend, nxt);
+  dma_stage<C>(g, slots, wave, p + NB - 1, plive, nxt);
   compute_stage<C, TN, TM>(cur, o, acc);
   // Keep each stage's MFMAs and folds inside the stage: interleaving them
   // with the next stage's only lengthens register lifetimes.
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// NB stage buffers (prefetch distance NB - 1); WPE waves per SIMD.
-template <int WN, int WM, int TN, int TM, int NB, int WPE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemm_mx_kernel(
+// NB stage buffers (prefetch distance NB - 1); WPE waves per SIMD.  KG K
+// groups of 4 waves: group k runs its own pipeline over the k-th part of the
+// workgroup's block pairs (both groups the same number of stages, the last
+// one possibly of zeros), and the groups' sums are added in group order at
+// the end -- twice the waves for a launch whose tiles alone leave the SIMDs
+// with less than one wave each, with no second launch to add partials.
+template <int WN, int WM, int TN, int TM, int NB, int WPE, int KG = 1>
+__global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemm_mx_kernel(
     GemmMulti gm) {
   using C = Cfg<WN, WM, TN, TM>;
-  // NB stage buffers in one array, indexed by compile-time constants only:
-  // a buffer's reads are the per-thread offsets plus a constant.
-  __shared__ __align__(1024) char lds[NB][C::STAGE];
-  const int wave = uniform(threadIdx.x >> 6);
+  // NB stage buffers per K group in one array, indexed by compile-time
+  // constants only (and the group): a buffer's reads are the per-thread
+  // offsets plus a constant.
+  __shared__ __align__(1024) char lds[KG][NB][C::STAGE];
+  const int wave_g = uniform(threadIdx.x >> 6);
+  const int kg = KG > 1 ? wave_g >> 2 : 0, wave = wave_g & 3;
   const int wn = wave % WN, wm = wave / WN;
   int bx = blockIdx.x, mat = 0;
   if (bx >= gm.gx0) {
@@ -338,26 +352,53 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
   Slots<C> slots;
   init_slots<C>(g, wave, nt0, mt0, slots);
   const StageOffs offs = stage_offsets<C, TN, TM>(wn, wm);
-  // Split z of the K range: block pairs [p0, pend).
+  // Split z of the K range: block pairs [p0, pend); K group kg: n stages from q0, those from
+  // qlive on of zeros.
   const int z = blockIdx.z;
   const int p0 = static_cast<int>(static_cast<long>(g.pp) * z / g.splits);
   const int pend = static_cast<int>(static_cast<long>(g.pp) * (z + 1) / g.splits);
+  const int n = (pend - p0 + KG - 1) / KG;
+  const int q0 = p0 + kg * n, qend = q0 + n, qlive = min(qend, pend);
+  char (&buf)[NB][C::STAGE] = lds[kg];
 #pragma unroll
-  for (int u = 0; u < NB - 1; u++) dma_stage<C>(g, slots, wave, p0 + u, pend, lds[u]);
+  for (int u = 0; u < NB - 1; u++) dma_stage<C>(g, slots, wave, q0 + u, qlive, buf[u]);
   // Unrolled by NB so every stage's buffer roles are static.
-  int p = p0;
-  for (; p + NB - 1 < pend; p += NB) {
+  int p = q0;
+  for (; p + NB - 1 < qend; p += NB) {
 #pragma unroll
     for (int u = 0; u < NB; u++)
-      pipeline_step<C, TN, TM, NB>(g, slots, wave, p + u, pend, lds[u], lds[(u + NB - 1) % NB], offs, acc);
+      pipeline_step<C, TN, TM, NB>(g, slots, wave, p + u, qlive, buf[u], buf[(u + NB - 1) % NB], offs, acc);
   }
 #pragma unroll
   for (int u = 0; u < NB - 1; u++)
-    if (p + u < pend)
-      pipeline_step<C, TN, TM, NB>(g, slots, wave, p + u, pend, lds[u], lds[(u + NB - 1) % NB], offs, acc);
-  // Drain the prefetches of stages past pend before the workgroup can exit
-  // (their LDS must not be written after it is released).
+    if (p + u < qend)
+      pipeline_step<C, TN, TM, NB>(g, slots, wave, p + u, qlive, buf[u], buf[(u + NB - 1) % NB], offs, acc);
+  // Drain the prefetches of stages past the range before the workgroup can
+  // exit (their LDS must not be written after it is released).
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  if constexpr (KG > 1) {
+    // Group 1's sums through the (now idle) stage buffers, added after group 0's.
+    __syncthreads();
+    float *xch = reinterpret_cast<float *>(&lds[0][0][0]);
+    static_assert(4 * TN * TM * 16 * 64 * sizeof(float) <= sizeof(lds), "exchange fits the stage buffers");
+    if (kg == 1) {
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+          for (int v = 0; v < 16; v++) xch[(((wave * TN + tn) * TM + tm) * 16 + v) * 64 + lane] = acc[tn][tm][v];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          acc[tn][tm][v] = acc[tn][tm][v] + xch[(((wave * TN + tn) * TM + tm) * 16 + v) * 64 + lane];
+  }
 
   // With split K the partial sums go to part[z] (assign); a second kernel
   // adds the splits in order and applies the caller's mode.
@@ -505,7 +546,7 @@ int splits_for_tiles(long tiles, size_t pp) {
   return splits;
 }
 
-template <int WN, int WM, int TN, int TM, int NB, int WPE>
+template <int WN, int WM, int TN, int TM, int NB, int WPE, int KG = 1>
 hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
   using C = Cfg<WN, WM, TN, TM>;
   int gx[3] = {0, 0, 0};
@@ -516,7 +557,7 @@ hipError_t launch_cfg(GemmMulti gm, int nmat, int splits, hipStream_t st) {
   gm.gx0 = gx[0];
   gm.gx1 = gx[1];
   const dim3 grid(static_cast<unsigned>(gx[0] + gx[1] + gx[2]), (gm.g[0].mt + C::MS - 1) / C::MS, splits);
-  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM, NB, WPE>), grid, dim3(kThreads), 0, st, gm);
+  hipLaunchKernelGGL((q4_gemm_mx_kernel<WN, WM, TN, TM, NB, WPE, KG>), grid, dim3(kThreads * KG), 0, st, gm);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   ReduceMulti r{};
@@ -555,18 +596,24 @@ static long gemm_tiles(const lgh_q4 *const *w, int nmat, size_t m) {
   return tiles * static_cast<long>(((m + 31) / 32 + MS - 1) / MS);
 }
 
-int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m) {
-  return splits_for_tiles<4, 1, 1, 1>(gemm_tiles<4, 1>(w, nmat, m), w[0]->pp);
+GemmPlan plan_q4_gemm(const lgh_q4 *const *w, int nmat, size_t m) {
+  GemmPlan plan;
+  const long tiles = gemm_tiles<4, 1>(w, nmat, m);
+  plan.splits = splits_for_tiles<4, 1, 1, 1>(tiles, w[0]->pp);
+  if (plan.splits == 1 && tiles < kKgTiles && w[0]->pp >= 2) plan.kgroups = 2;
+  return plan;
 }
 
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
-                          int splits, float *part, size_t part_floats, hipStream_t st) {
+                          GemmPlan plan, float *part, size_t part_floats, hipStream_t st) {
   if (m == 0 || nmat < 1 || nmat > 3) return m == 0 ? hipSuccess : hipErrorInvalidValue;
   size_t rows = 0;
   for (int j = 0; j < nmat; j++) rows += w[j]->n;
   if (rows == 0) return hipSuccess;
+  const int splits = plan.splits;
   if (splits < 1 || (splits > 1 && (!part || static_cast<size_t>(splits) * m * rows > part_floats)))
     return hipErrorInvalidValue;
+  if (plan.kgroups != 1 && (plan.kgroups != 2 || splits != 1 || w[0]->pp < 2)) return hipErrorInvalidValue;
   const size_t mt = (m + 31) / 32;
   GemmMulti gm{};
   size_t off = 0;
@@ -598,6 +645,13 @@ hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, 
   // idle: M=512, K=2048, N=8192 (512) 32.2 -> 32.5 us, M=256, N=10752 (336)
   // 25.8 -> 29.3 us, M=1024, K=10752, N=2048 (256; split K otherwise) 82.6
   // -> 94.4 us.
+  // Few tiles and no split K (planned for the whole call: the two groups' sums
+  // are added at the end, another f32 order): two K groups per workgroup, 8
+  // waves, 72 KB of LDS.  Whole calls, against one group: K=2048, N=8192, M=65
+  // / 128 / 192: 17.1 / 17.8 / 20.3 -> 14.4 / 15.3 / 19.4 us; N=10752, M=65
+  // 18.3 -> 15.6 us; K=1536, N=8192, M=65 13.7 -> 12.1 us; K=2048, N=2048,
+  // M=512 17.3 -> 16.2 us; N=2048, K=1536, M=128 12.6 -> 11.7 us.
+  if (plan.kgroups == 2) return launch_cfg<4, 1, 1, 1, 3, 4, 2>(gm, nmat, 1, st);
   if (splits == 1 && gemm_tiles<4, 2>(w, nmat, m) >= kWideWgs) return launch_cfg<4, 1, 1, 2, 3, 3>(gm, nmat, 1, st);
   // Otherwise 128 x 32 (4 waves, one 32 x 32 tile each, 108 VGPRs, 4 waves
   // per SIMD): the most workgroups resident to cover the stage loads.

@@ -226,15 +226,19 @@ hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int
 
 // GEMM on an activation operand image: y[j][m][n_j] (+)= x[m][k] . W[j]^T for
 // 1..3 matrices with the same k, one launch (the workgroups of all matrices
-// in one grid, one split-K reduce).  plan_q4_gemm_splits() is the number of K
-// splits a call of m tokens wants; the caller passes the count it planned
-// (the split count fixes the f32 summation order, so a call cut into token
-// chunks keeps the count of the whole call), and `part` must hold
-// splits * m * (sum of n) floats when splits > 1 (hipErrorInvalidValue
+// in one grid, one split-K reduce).  plan_q4_gemm() is what a call of m
+// tokens wants: the number of K splits across workgroups and of K groups
+// inside one.  Both fix the f32 summation order, so the caller passes the plan
+// of the whole call to every token chunk it cuts the call into.  `part` must
+// hold splits * m * (sum of n) floats when splits > 1 (hipErrorInvalidValue
 // otherwise, nothing launched).
-int plan_q4_gemm_splits(const lgh_q4 *const *w, int nmat, size_t m);
+struct GemmPlan {
+  int splits = 1;   // K splits across workgroups, added by a reduce launch
+  int kgroups = 1;  // 1, or 2 (splits == 1, >= 2 block pairs): K halves in one workgroup
+};
+GemmPlan plan_q4_gemm(const lgh_q4 *const *w, int nmat, size_t m);
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
-                          int splits, float *part, size_t part_floats, hipStream_t stream);
+                          GemmPlan plan, float *part, size_t part_floats, hipStream_t stream);
 
 // Measurement probes: an empty kernel of `wgs` workgroups, and a plain read
 // of `bytes` (a multiple of 16, 16-byte aligned) with per_thread (1, 2, 4, 8)
