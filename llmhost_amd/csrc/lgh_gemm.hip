@@ -40,6 +40,7 @@ constexpr size_t kSplitMinPairs = 64;  // K >= 4096
 constexpr size_t kSplitPairs = 16;     // K >= 1024 per split
 constexpr long kWideWgs = 640;  // 128 x 64 workgroup tiles from this many of them (2.5 per CU), no split K
 constexpr long kKgTiles = 512;  // two K groups per workgroup below this many 128 x 32 tiles (no split K)
+constexpr long kKg4Tiles = 256;  // four below this many
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]
@@ -313,10 +314,10 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &g, const Slots<C> 
 
 // NB stage buffers (prefetch distance NB - 1); WPE waves per SIMD.  KG K
 // groups of 4 waves: group k runs its own pipeline over the k-th part of the
-// workgroup's block pairs (both groups the same number of stages, the last
-// one possibly of zeros), and the groups' sums are added in group order at
-// the end -- twice the waves for a launch whose tiles alone leave the SIMDs
-// with less than one wave each, with no second launch to add partials.
+// workgroup's block pairs (every group the same number of stages, the last
+// ones possibly of zeros), and the groups' sums are added in a fixed tree at
+// the end -- KG times the waves for a launch whose tiles alone leave the
+// SIMDs with less than one wave each, with no second launch to add partials.
 template <int WN, int WM, int TN, int TM, int NB, int WPE, int KG = 1>
 __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemm_mx_kernel(
     GemmMulti gm) {
@@ -377,27 +378,38 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(W
   // exit (their LDS must not be written after it is released).
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   if constexpr (KG > 1) {
-    // Group 1's sums through the (now idle) stage buffers, added after group 0's.
-    __syncthreads();
+    // The groups' sums through the (now idle) stage buffers, a tree in group
+    // order: at level h group kg + h's sums are added to group kg's (kg < h),
+    // so four groups give (g0 + g2) + (g1 + g3).  Every wave takes every
+    // barrier; only group 0 goes on to the stores.
+    constexpr int kSlot = 4 * TN * TM * 16 * 64;
+    static_assert((KG / 2) * kSlot * sizeof(float) <= sizeof(lds), "exchange fits the stage buffers");
     float *xch = reinterpret_cast<float *>(&lds[0][0][0]);
-    static_assert(4 * TN * TM * 16 * 64 * sizeof(float) <= sizeof(lds), "exchange fits the stage buffers");
-    if (kg == 1) {
 #pragma unroll
-      for (int tn = 0; tn < TN; tn++)
+    for (int h = KG / 2; h >= 1; h /= 2) {
+      __syncthreads();
+      if (kg >= h && kg < 2 * h) {
+        float *slot = xch + (kg - h) * kSlot;
 #pragma unroll
-        for (int tm = 0; tm < TM; tm++)
+        for (int tn = 0; tn < TN; tn++)
 #pragma unroll
-          for (int v = 0; v < 16; v++) xch[(((wave * TN + tn) * TM + tm) * 16 + v) * 64 + lane] = acc[tn][tm][v];
+          for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) slot[(((wave * TN + tn) * TM + tm) * 16 + v) * 64 + lane] = acc[tn][tm][v];
+      }
+      __syncthreads();
+      if (kg < h) {
+        const float *slot = xch + kg * kSlot;
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+          for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+              acc[tn][tm][v] = acc[tn][tm][v] + slot[(((wave * TN + tn) * TM + tm) * 16 + v) * 64 + lane];
+      }
     }
-    __syncthreads();
-    if (kg == 1) return;
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++)
-#pragma unroll
-      for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-        for (int v = 0; v < 16; v++)
-          acc[tn][tm][v] = acc[tn][tm][v] + xch[(((wave * TN + tn) * TM + tm) * 16 + v) * 64 + lane];
+    if (kg != 0) return;
   }
 
   // With split K the partial sums go to part[z] (assign); a second kernel
@@ -600,7 +612,10 @@ GemmPlan plan_q4_gemm(const lgh_q4 *const *w, int nmat, size_t m) {
   GemmPlan plan;
   const long tiles = gemm_tiles<4, 1>(w, nmat, m);
   plan.splits = splits_for_tiles<4, 1, 1, 1>(tiles, w[0]->pp);
-  if (plan.splits == 1 && tiles < kKgTiles && w[0]->pp >= 2) plan.kgroups = 2;
+  if (plan.splits == 1 && tiles < kKg4Tiles && w[0]->pp >= 4)
+    plan.kgroups = 4;
+  else if (plan.splits == 1 && tiles < kKgTiles && w[0]->pp >= 2)
+    plan.kgroups = 2;
   return plan;
 }
 
@@ -613,7 +628,9 @@ hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, 
   const int splits = plan.splits;
   if (splits < 1 || (splits > 1 && (!part || static_cast<size_t>(splits) * m * rows > part_floats)))
     return hipErrorInvalidValue;
-  if (plan.kgroups != 1 && (plan.kgroups != 2 || splits != 1 || w[0]->pp < 2)) return hipErrorInvalidValue;
+  if (plan.kgroups != 1 && ((plan.kgroups != 2 && plan.kgroups != 4) || splits != 1 ||
+                            w[0]->pp < static_cast<size_t>(plan.kgroups)))
+    return hipErrorInvalidValue;
   const size_t mt = (m + 31) / 32;
   GemmMulti gm{};
   size_t off = 0;
@@ -646,11 +663,16 @@ hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, 
   // 25.8 -> 29.3 us, M=1024, K=10752, N=2048 (256; split K otherwise) 82.6
   // -> 94.4 us.
   // Few tiles and no split K (planned for the whole call: the two groups' sums
-  // are added at the end, another f32 order): two K groups per workgroup, 8
+  // are added at the end, another f32 order): K groups per workgroup; two: 8
   // waves, 72 KB of LDS.  Whole calls, against one group: K=2048, N=8192, M=65
   // / 128 / 192: 17.1 / 17.8 / 20.3 -> 14.4 / 15.3 / 19.4 us; N=10752, M=65
   // 18.3 -> 15.6 us; K=1536, N=8192, M=65 13.7 -> 12.1 us; K=2048, N=2048,
-  // M=512 17.3 -> 16.2 us; N=2048, K=1536, M=128 12.6 -> 11.7 us.
+  // M=512 17.3 -> 16.2 us; N=2048, K=1536, M=128 12.6 -> 11.7 us.  Below 256
+  // tiles four groups (16 waves, 144 KB of LDS), against two: N=1536, K=2048,
+  // M=65 / 128 / 256 13.3 / 13.5 / 14.1 -> 12.7 / 12.7 / 13.5 us; N=2048,
+  // K=1536, M=65 11.7 -> 11.4 us; N=2048, K=2048, M=256 14.2 -> 13.6 us; equal
+  // at N=8192 (192 tiles at M=65).
+  if (plan.kgroups == 4) return launch_cfg<4, 1, 1, 1, 3, 4, 4>(gm, nmat, 1, st);
   if (plan.kgroups == 2) return launch_cfg<4, 1, 1, 1, 3, 4, 2>(gm, nmat, 1, st);
   if (splits == 1 && gemm_tiles<4, 2>(w, nmat, m) >= kWideWgs) return launch_cfg<4, 1, 1, 2, 3, 3>(gm, nmat, 1, st);
   // Otherwise 128 x 32 (4 waves, one 32 x 32 tile each, 108 VGPRs, 4 waves

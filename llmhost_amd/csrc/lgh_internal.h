@@ -234,7 +234,7 @@ hipError_t launch_act_quant(const float *x, size_t m, size_t k, int per_row, int
 // otherwise, nothing launched).
 struct GemmPlan {
   int splits = 1;   // K splits across workgroups, added by a reduce launch
-  int kgroups = 1;  // 1, or 2 (splits == 1, >= 2 block pairs): K halves in one workgroup
+  int kgroups = 1;  // 1, 2 or 4 (splits == 1, >= kgroups block pairs): K parts in one workgroup
 };
 GemmPlan plan_q4_gemm(const lgh_q4 *const *w, int nmat, size_t m);
 hipError_t launch_q4_gemm(const lgh_q4 *const *w, int nmat, const uint8_t *mxa, float *const *y, size_t m, int mode,
