@@ -41,6 +41,7 @@ constexpr size_t kSplitPairs = 16;     // K >= 1024 per split
 constexpr long kWideWgs = 640;  // 128 x 64 workgroup tiles from this many of them (2.5 per CU), no split K
 constexpr long kKgTiles = 512;  // two K groups per workgroup below this many 128 x 32 tiles (no split K)
 constexpr long kKg4Tiles = 256;  // four below this many
+constexpr size_t kKgSplitPairs = 128;  // two K groups replace a split in two up to this many block pairs
 
 struct GemmArgs {
   const uint8_t *wmx;  // weight operand image [nt][pp]
@@ -611,10 +612,19 @@ static long gemm_tiles(const lgh_q4 *const *w, int nmat, size_t m) {
 GemmPlan plan_q4_gemm(const lgh_q4 *const *w, int nmat, size_t m) {
   GemmPlan plan;
   const long tiles = gemm_tiles<4, 1>(w, nmat, m);
-  plan.splits = splits_for_tiles<4, 1, 1, 1>(tiles, w[0]->pp);
-  if (plan.splits == 1 && tiles < kKg4Tiles && w[0]->pp >= 4)
+  const size_t pp = w[0]->pp;
+  plan.splits = splits_for_tiles<4, 1, 1, 1>(tiles, pp);
+  // Two K groups instead of two splits on rows of <= 128 block pairs: the
+  // same waves, no partials and no reduce launch.  Whole calls, interleaved
+  // A/B: K=4096, N=4096, M=256 25.7 -> 22.2 us; K=8192, N=8192, M=128 37.4 ->
+  // 35.4 us.  On longer rows the split stays ahead (K=10752, N=2048, M=512
+  // 47.9 against 48.6 us, bit-identical: the halves are the same), and in
+  // place of one of four or more splits the groups lose (K=8192, N=1536,
+  // M=512: 4 splits 33.5 us, 2 groups x 2 splits 35.0 us).
+  if (plan.splits == 2 && pp <= kKgSplitPairs) plan.splits = 1;
+  if (plan.splits == 1 && tiles < kKg4Tiles && pp >= 4)
     plan.kgroups = 4;
-  else if (plan.splits == 1 && tiles < kKgTiles && w[0]->pp >= 2)
+  else if (plan.splits == 1 && tiles < kKgTiles && pp >= 2)
     plan.kgroups = 2;
   return plan;
 }
