@@ -850,7 +850,7 @@ static int mma_chunked(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int 
     Carve cv;
     l.o_ci = cv.take(mt * pq * 2 * 1024);
     l.o_si = cv.take(mt * pq * 256);
-    l.o_rs = cv.take(2 * c * sizeof(float));
+    l.o_rs = cv.take(c * sizeof(float));
     l.bytes = cv.off;
     return l;
   };
@@ -947,7 +947,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     const size_t mt = (m + 15) / 16, pq = (bpr + 3) / 4;
     Carve cv;
     const size_t o_ci = cv.take(mt * pq * 2 * 1024), o_si = cv.take(mt * pq * 256);
-    const size_t o_rs = cv.take(2 * m * sizeof(float));
+    const size_t o_rs = cv.take(m * sizeof(float));
     char *ws = nullptr;
     if (int r = wsp.get(cv.off, &ws)) return r;
     auto *ci = reinterpret_cast<uint8_t *>(ws + o_ci);
@@ -998,7 +998,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
     l.part_floats = splits > 1 ? static_cast<size_t>(splits) * c * rows : 0;
     Carve cv;
     l.o_mx = cv.take((c + 31) / 32 * rec_per_tile);
-    l.o_rs = cv.take(2 * c * sizeof(float));
+    l.o_rs = cv.take(c * sizeof(float));
     l.o_part = cv.take(l.part_floats * sizeof(float));
     l.bytes = cv.off;
     return l;

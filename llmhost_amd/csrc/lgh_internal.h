@@ -94,21 +94,20 @@ constexpr uint32_t kImageLayout = (1u << 16) | static_cast<uint32_t>(kMxWRec);
 
 // Weight operand image from the repacked nibble/scale planes (load time).
 hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t stream);
-// The elementwise step an activation image kernel applies to x before ActQ8:
+// The elementwise step an activation image launch applies to x before ActQ8:
 // none, h = silu(x) * u (u [m][k]: the FFN's down-projection input, formed in
-// place of the silu_mul launch) or rms_norm(x, nw, eps) (nw [k], ops.rs:8-23:
-// nw * (x * scale_t) with the row scales from a one-wave-per-row kernel, in
-// place of rms_norm writing the normed rows).  Either way the image equals
-// the op sequence's bit for bit.  nscale is set by the launchers.
+// place of the silu_mul launch) or rms_norm(x, nw, eps) (nw [k], ops.rs:8-23,
+// in place of rms_norm writing the normed rows: one kernel forms each row's
+// scale and writes its image).  Either way the image equals the op
+// sequence's bit for bit.
 struct ActPrologue {
   const float *u = nullptr;
   const float *nw = nullptr;
   float eps = 0.0f;
-  const float *nscale = nullptr;
 };
 // Activation operand image: quantize the rows of x[m][k] (after the prologue)
 // per ActQ8 (per_row selects the mode) straight into mt*pp records.  scratch:
-// 2*m floats (row scales).
+// m floats (PerRow scales).
 hipError_t launch_act_quant_mx(const float *x, ActPrologue pro, size_t m, size_t k, int per_row, uint8_t *mxa,
                                float *scratch, hipStream_t stream);
 // Same record layout from already-quantized int8 activations aq [m][k] and

@@ -23,17 +23,11 @@ __device__ __forceinline__ float4 silu_mul4(float4 g, float4 u) {
   return make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
 }
 
-// The elementwise prologue of an image kernel on float4 f of x (float4 fr of
-// token t's row): h = silu(x) * u, or the rms_norm output nw * (x * scale_t)
-// with the row's scale from row_norm_kernel; uniform branches.
-__device__ __forceinline__ void apply_prologue(const ActPrologue &pro, int t, size_t fr, size_t f, float4 &v) {
-  if (pro.u) {
-    v = silu_mul4(v, reinterpret_cast<const float4 *>(pro.u)[f]);
-  } else if (pro.nw) {
-    const float s = pro.nscale[t];
-    const float4 w = reinterpret_cast<const float4 *>(pro.nw)[fr];
-    v = make_float4(w.x * (v.x * s), w.y * (v.y * s), w.z * (v.z * s), w.w * (v.w * s));
-  }
+// The elementwise prologue of an image kernel on float4 f of x: h = silu(x) *
+// u when u is set (uniform branch).  The norm has a kernel of its own
+// (norm_image_kernel).
+__device__ __forceinline__ void apply_prologue(const ActPrologue &pro, size_t f, float4 &v) {
+  if (pro.u) v = silu_mul4(v, reinterpret_cast<const float4 *>(pro.u)[f]);
 }
 
 // Row amax / 127 of x, or (u not null) of silu(x) * u.
@@ -315,8 +309,8 @@ __global__ __launch_bounds__(kThreads) void act_quant_mx_kernel(const float *__r
     const float4 *src = reinterpret_cast<const float4 *>(x) + f;
     a = src[0];
     b = src[1];
-    apply_prologue(pro, t, blk * 8 + 2 * g, f, a);
-    apply_prologue(pro, t, blk * 8 + 2 * g + 1, f + 1, b);
+    apply_prologue(pro, f, a);
+    apply_prologue(pro, f + 1, b);
   }
   s_hl[tid] = kHlTable.v[tid];
   __syncthreads();  // the table
@@ -398,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void act_quant_mma_kernel(const float *__
   if (ok) {
     const size_t f = (static_cast<size_t>(t) * bpr + b) * 8 + g8;
     v = reinterpret_cast<const float4 *>(x)[f];
-    apply_prologue(pro, t, b * 8 + g8, f, v);
+    apply_prologue(pro, f, v);
   }
   const bool pr = ok && per_row;
   const float rs = pr ? row_scale[t] : 0.0f;
@@ -432,71 +426,131 @@ __global__ __launch_bounds__(kThreads) void act_codes_mma_kernel(const int8_t *_
   if (g8 == 0) scales[((static_cast<size_t>(t >> 4) * pq + (b >> 2)) * 16 + (t & 15)) * 4 + (b & 3)] = ok ? as[blk] : 0.0f;
 }
 
-// ---- rms_norm scales for the activation images --------------------------------
-// The row's sum of squares in exactly rms_norm_kernel's order (256 threads:
-// thread i adds the f64 squares of elements i, i + 256, ... in turn, each
-// wave's 64 partials meet in wave_sum_dpp64's tree, the 4 wave sums are added
-// in order), so the scale -- and every normed value nw * (x * scale) -- equals
-// the op sequence's bit for bit.  Element 4 lane + c + 256 j sits in component
-// c of the lane's float4 lane + 64 j, i.e. belongs to thread 4 lane + c: the
-// lane keeps those 4 partials (j in order), and thread 64 v + L's partial is
-// fetched into lane L to replay wave v's tree.
-__device__ __forceinline__ double replay_256_thread_sum(double p0, double p1, double p2, double p3) {
-  const int lane = threadIdx.x & (kWave - 1), sel = lane & 3;
-  double tot = 0.0;
+// ---- rms_norm in the activation images ---------------------------------------
+// rms_norm (ops.rs:8-23) and an activation image in one launch, one
+// workgroup per token row of the padded token range.  The sum of squares is
+// formed exactly as rms_norm_kernel forms it (thread i adds the f64 squares
+// of elements i, i + 256, ... in turn; DPP wave trees; the 4 wave sums in
+// order), so the scale and every normed value nw * (x * scale) equal the op
+// sequence's bit for bit.  The normed row is then quantized by 8-lane groups
+// (act_quant_group8: the codes and scales of the image kernels' quantizers)
+// and written to the row's places in the image: the GEMM's operand records
+// (MX, 32-token tiles) or the matrix-core batch layout (16-token tiles).
+// Rows past m and blocks past bpr get code 0 and scale 0, as the image
+// kernels write them.  Workgroups are dealt round robin to the 8 XCDs, so
+// workgroup b takes token (b / 8) % TT of tile 8 (b / (8 TT)) + b % 8: the
+// rows of one tile, which share the image's cache lines, are written through
+// one XCD's L2.
+template <bool MX>
+__global__ __launch_bounds__(kThreads) void norm_image_kernel(const float *__restrict__ x,
+                                                              const float *__restrict__ nw, double inv_k, float eps,
+                                                              int m, int bpr, int nblk, int mt, int per_row,
+                                                              uint8_t *__restrict__ img, float *__restrict__ scales) {
+  constexpr int TT = MX ? 32 : 16;
+  constexpr int kRound = kThreads / 8;  // blocks per round of 8-lane groups
+  constexpr int kPre = 4;               // rounds whose loads are in flight together
+  const int wg = static_cast<int>(blockIdx.x);
+  const int tile = 8 * (wg / (8 * TT)) + (wg & 7);
+  if (tile >= mt) return;  // whole workgroups
+  const int t = tile * TT + (wg >> 3) % TT;
+  const bool live = t < m;  // uniform
+  const int k = bpr * 32;
+  const uint32_t row_bytes = static_cast<uint32_t>(k) * 4u;
+  // Rows past m read as zeros (a resource of size 0) and are stored as zeros.
+  const auto xr = make_rsrc(x + static_cast<size_t>(live ? t : 0) * k, live ? row_bytes : 0u);
+  const auto nr = make_rsrc(nw, row_bytes);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int g8 = tid & 7, grp = tid >> 3;
+  // The first rounds' float4s of x and nw (blocks past bpr read 0), requested
+  // before the sum of squares so they arrive while it is formed.
+  float4 xa[kPre], wa[kPre];
+  auto load_rounds = [&](int b0) {
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int src = 16 * v + (lane >> 2);
-    const double t0 = __shfl(p0, src, kWave), t1 = __shfl(p1, src, kWave);
-    const double t2 = __shfl(p2, src, kWave), t3 = __shfl(p3, src, kWave);
-    const double mine = sel == 0 ? t0 : sel == 1 ? t1 : sel == 2 ? t2 : t3;
-    tot += wave_sum_dpp64(mine);
-  }
-  return tot;
-}
-
-constexpr int kRnBatch = 8;  // float4s per lane in flight
-
-// One wave per token row (4 per workgroup): nscale[t] = the rms_norm scale of
-// row t (ops.rs:12-17) and, with row_scale, the PerRow scale of the normed row
-// (amax(nw * (x * scale)) / 127, as row_amax_kernel over rms_norm's output).
-// The image kernels then quantize nw * (x * nscale[t]) element by element.
-__global__ __launch_bounds__(kThreads) void row_norm_kernel(const float *__restrict__ x, const float *__restrict__ nw,
-                                                            double inv_k, float eps, int m, int bpr, float *nscale,
-                                                            float *row_scale) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int t = static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x >> 6);
-  if (t >= m) return;  // whole waves
-  const uint32_t row_bytes = static_cast<uint32_t>(bpr) * 128u;
-  const auto xr = make_rsrc(x + static_cast<size_t>(t) * bpr * 32, row_bytes);
-  const int nj = (bpr * 8 + 63) / 64;  // float4s per lane (past the row: 0 through the range check)
-  double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
-  for (int j0 = 0; j0 < nj; j0 += kRnBatch) {
-    float4 v[kRnBatch];
+    for (int u = 0; u < kPre; u++) {
+      const uint32_t off = static_cast<uint32_t>((b0 + kRound * u + grp) * 8 + g8) * 16u;
+      xa[u] = buf_load_f4(xr, off);
+      wa[u] = buf_load_f4(nr, off);
+    }
+  };
+  load_rounds(0);
+  // Thread i: the squares of elements i, i + 256, ... in order, 8 loads in
+  // flight; elements past k read 0 and add +0.0, which changes no sum.
+  double ss = 0.0;
+  for (int i0 = 0; i0 < k; i0 += kThreads * 8) {
+    float v[8];
 #pragma unroll
-    for (int i = 0; i < kRnBatch; i++) v[i] = buf_load_f4(xr, static_cast<uint32_t>(lane + 64 * (j0 + i)) * 16u);
+    for (int u = 0; u < 8; u++) v[u] = buf_load_f32(xr, static_cast<uint32_t>(i0 + tid + kThreads * u) * 4u);
 #pragma unroll
-    for (int i = 0; i < kRnBatch; i++) {  // squares past the row add +0.0 exactly
-      const double a = v[i].x, b = v[i].y, c = v[i].z, d = v[i].w;
-      p0 += a * a;
-      p1 += b * b;
-      p2 += c * c;
-      p3 += d * d;
+    for (int u = 0; u < 8; u++) {
+      const double d = v[u];
+      ss += d * d;
     }
   }
-  const float scale = rms_scale(replay_256_thread_sum(p0, p1, p2, p3), inv_k, eps);
-  if (lane == 0) nscale[t] = scale;
-  if (!row_scale) return;  // uniform
-  const auto nr = make_rsrc(nw, row_bytes);
-  float mx = 0.0f;
-  for (int j = 0; j < nj; j++) {
-    const uint32_t off = static_cast<uint32_t>(lane + 64 * j) * 16u;
-    const float4 a = buf_load_f4(xr, off), w = buf_load_f4(nr, off);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w.x * (a.x * scale)), fabsf(w.y * (a.y * scale))),
-                         fmaxf(fabsf(w.z * (a.z * scale)), fabsf(w.w * (a.w * scale)))));
+  __shared__ double s_ss[kWaves];
+  __shared__ float s_mx[kWaves];
+  ss = wave_sum_dpp64(ss);
+  if (lane == 0) s_ss[wave] = ss;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int i = 0; i < kWaves; i++) tot += s_ss[i];
+  const float scale = rms_scale(tot, inv_k, eps);
+  float rs = 0.0f;
+  if (per_row) {  // amax(nw * (x * scale)) / 127, as row_amax_kernel over the normed rows
+    float mx = 0.0f;
+    for (int f = tid; f < k / 4; f += kThreads) {
+      const float4 a = buf_load_f4(xr, static_cast<uint32_t>(f) * 16u);
+      const float4 w = buf_load_f4(nr, static_cast<uint32_t>(f) * 16u);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w.x * (a.x * scale)), fabsf(w.y * (a.y * scale))),
+                           fmaxf(fabsf(w.z * (a.z * scale)), fabsf(w.w * (a.w * scale)))));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) s_mx[wave] = mx;
+    __syncthreads();
+    rs = div127_rn(fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3])));
   }
-  mx = wave_max(mx);
-  if (lane == 0) row_scale[t] = div127_rn(mx);
+  for (int b0 = 0; b0 < nblk; b0 += kRound * kPre) {
+    if (b0 > 0) load_rounds(b0);
+#pragma unroll
+    for (int u = 0; u < kPre; u++) {
+      const int blk = b0 + kRound * u + grp;
+      const bool ok = live && blk < bpr;
+      const float4 a = xa[u], w = wa[u];
+      const float4 v = ok ? make_float4(w.x * (a.x * scale), w.y * (a.y * scale), w.z * (a.z * scale),
+                                        w.w * (a.w * scale))
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float sc;
+      int sum;
+      const int q = act_quant_group8(v, ok && per_row, rs, sc, sum);
+      if (blk >= nblk) continue;  // whole 8-lane groups
+      if constexpr (MX) {
+        uint32_t vh, vl;
+        codes24_hl(q, vh, vl);
+        uint8_t *rec = img + (static_cast<size_t>(tile) * (nblk / 2) + (blk >> 1)) * kMxARec;
+        store_hl_group8(rec, blk & 1, t & 31, vh, vl);
+        if (g8 == 0) reinterpret_cast<float *>(rec + 4 * kMxTile)[(blk & 1) * 32 + (t & 31)] = ok ? sc : 0.0f;
+      } else {
+        const int pq = nblk / 4;
+        const size_t pair = static_cast<size_t>(tile) * (2 * pq) + (blk >> 1);
+        const int ln = (t & 15) + 16 * (g8 >> 1);
+        *reinterpret_cast<int *>(img + (pair * 64 + ln) * 16 + (blk & 1) * 8 + (g8 & 1) * 4) = q;
+        if (g8 == 0)
+          scales[((static_cast<size_t>(tile) * pq + (blk >> 2)) * 16 + (t & 15)) * 4 + (blk & 3)] = ok ? sc : 0.0f;
+      }
+    }
+  }
+}
+
+template <bool MX>
+hipError_t launch_norm_image(const float *x, const ActPrologue &pro, size_t m, size_t k, int per_row, int nblk,
+                             uint8_t *img, float *scales, hipStream_t st) {
+  constexpr size_t TT = MX ? 32 : 16;
+  const size_t mt = (m + TT - 1) / TT;
+  const size_t wgs = (mt + 7) / 8 * 8 * TT;
+  hipLaunchKernelGGL(norm_image_kernel<MX>, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, st, x, pro.nw,
+                     1.0 / static_cast<double>(k), pro.eps, static_cast<int>(m), static_cast<int>(k / 32), nblk,
+                     static_cast<int>(mt), per_row, img, scales);
+  return hipGetLastError();
 }
 
 inline unsigned blocks_for(size_t items, unsigned per) {
@@ -514,20 +568,11 @@ hipError_t launch_q4_mx_pack(const lgh_q4 *w, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The row statistics an image kernel needs before it starts: the PerRow scale
-// (row_amax_kernel over x or silu(x) * u) or, for the norm, the rms_norm
-// scales and the PerRow scale of the normed rows (row_norm_kernel).
-// scratch: 2 * m floats; on return pro.nscale is set for the norm.
-hipError_t row_stats(const float *x, ActPrologue &pro, size_t m, size_t k, int per_row, float *scratch,
+// The PerRow scale an image kernel needs before it starts (row_amax_kernel
+// over x or silu(x) * u).  scratch: m floats.
+hipError_t row_stats(const float *x, const ActPrologue &pro, size_t m, size_t k, int per_row, float *scratch,
                      const float **row_scale, hipStream_t st) {
   *row_scale = per_row ? scratch : nullptr;
-  if (pro.nw) {
-    pro.nscale = scratch + m;
-    hipLaunchKernelGGL(row_norm_kernel, dim3(static_cast<unsigned>((m + kWaves - 1) / kWaves)), dim3(kThreads), 0, st,
-                       x, pro.nw, 1.0 / static_cast<double>(k), pro.eps, static_cast<int>(m),
-                       static_cast<int>(k / 32), scratch + m, per_row ? scratch : nullptr);
-    return hipGetLastError();
-  }
   if (!per_row) return hipSuccess;
   hipLaunchKernelGGL(row_amax_kernel, dim3(static_cast<unsigned>(m)), dim3(kThreads), 0, st, x, pro.u,
                      static_cast<int>(k), scratch);
@@ -538,6 +583,7 @@ hipError_t launch_act_quant_mx(const float *x, ActPrologue pro, size_t m, size_t
                                float *scratch, hipStream_t st) {
   const size_t bpr = k / 32, pp = (bpr + 1) / 2, mt = (m + 31) / 32;
   if (m == 0 || bpr == 0) return hipSuccess;
+  if (pro.nw) return launch_norm_image<true>(x, pro, m, k, per_row, static_cast<int>(2 * pp), mxa, nullptr, st);
   const float *rs = nullptr;
   if (hipError_t e = row_stats(x, pro, m, k, per_row, scratch, &rs, st)) return e;
   const size_t recs = mt * pp;  // < 2^31: the image is below kMxMaxBytes
@@ -551,6 +597,7 @@ hipError_t launch_act_quant_mma(const float *x, ActPrologue pro, size_t m, size_
                                 float *scales, float *scratch, hipStream_t st) {
   const size_t bpr = k / 32, pq = (bpr + 3) / 4, mt = (m + 15) / 16;
   if (m == 0 || bpr == 0) return hipSuccess;
+  if (pro.nw) return launch_norm_image<false>(x, pro, m, k, per_row, static_cast<int>(4 * pq), codes, scales, st);
   const float *rs = nullptr;
   if (hipError_t e = row_stats(x, pro, m, k, per_row, scratch, &rs, st)) return e;
   const size_t groups = mt * 16 * pq * 4;
