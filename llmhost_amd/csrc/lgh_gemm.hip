@@ -147,7 +147,7 @@ __device__ __forceinline__ uint32_t lds_addr(const char *p) {
 // tiles past the image and of padding slots are >= 2^31 (out of range ->
 // zeros), and a stage p >= plive (prefetched past the end of the range and
 // never computed, or a stage a K group runs only to keep its barriers in step
-// with the other group's) loads zeros: its loads go through a resource of
+// with the other groups') loads zeros: its loads go through a resource of
 // size 0 (every offset out of range) with soffset 0.  Either way the stage
 // issues its WPW loads, so the vmcnt waits keep counting stages, and the
 // VGPR offsets stay the loop-invariant ones.
