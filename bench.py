@@ -840,7 +840,7 @@ def main():
     sections.append(("gemm_m_sweep_k2048_n8192", "Q4 GEMM M sweep across the route boundaries (K=2048, N=8192)",
                      lambda: [{k2: round(v, 3) if isinstance(v, float) else v
                                for k2, v in gemm_case(gb, m, 8192, 2048, 20, 900 + m).items() if k2 != "samples_us"}
-                              for m in (32, 48, 56, 64, 65, 72, 80, 96, 112, 128)]))
+                              for m in (32, 48, 49, 56, 64, 65, 72, 80, 96, 97, 112, 128)]))
     sections += [
         ("q8_gemv_k1536_n1536", "q8 gemv", lambda: q8_case(gb, 200)),
         ("q4_gemv_k1536_n1536", "Q4 GEMV K=N=1536 (the target's smallest shape)",
