@@ -78,6 +78,26 @@ def test_gemm_below_wide_threshold(gpu_ctx, oracle, m, n, k, mode, per_row):
     test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 31 * m + n + k + mode)
 
 
+# Launches of fewer than 512 tiles of 128 x 32 that are not split run K groups inside the
+# workgroup (four below 256 tiles with >= 4 block pairs, else two), and two K groups take the
+# place of a two-way split on rows of 64..128 block pairs.  Pair counts that do not divide by the
+# group count give groups of unequal length, the last ones partly or wholly without pairs.
+K_GROUPS = [(512, 2048, 1536),  # 256 tiles, 24 pairs: two groups of 12
+            (256, 4096, 4096),  # 256 tiles, 64 pairs: two groups in place of two splits
+            (300, 4096, 4096),  # 320 tiles, 64 pairs: the same with a ragged last token tile
+            (130, 1000, 2080),  # 40 tiles, 33 pairs: four groups of 9, 9, 9 and 6 pairs
+            (100, 3000, 224),   # 96 tiles, 4 pairs: four groups of one pair
+            (65, 256, 96),      # 6 tiles, 2 pairs: two groups of one pair
+            (97, 200, 288)]     # 8 tiles, 5 pairs: four groups of 2, 2, 1 and 0 pairs
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("m,n,k", K_GROUPS)
+def test_gemm_k_groups(gpu_ctx, oracle, m, n, k, mode, per_row):
+    test_gemm_sweep(gpu_ctx, oracle, m, n, k, mode, per_row, 13 * m + n + k + mode)
+
+
 @pytest.mark.parametrize("tokens", [2000, 256])  # 128 x 64 tiles (84 N groups x 32); 128 x 32 (84 x 8)
 def test_gemm_large_routes_three_matrices(gpu_ctx, oracle, tokens):
     k, rows = 64, (4096, 4096, 2560)
