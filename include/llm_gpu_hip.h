@@ -220,7 +220,8 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
  * comes from one fixed device array of LGH_NOALLOC_SCRATCH_BYTES per GPU,
  * held until the process ends; the call allocates, frees and synchronizes
  * nothing.  On the GEMM route (65 or more tokens) token chunks shrink until
- * their scratch fits, keeping the split-K count of the whole call; a call
+ * their scratch fits, keeping the whole call's plan (split-K count and K
+ * groups per workgroup, which fix the f32 summation order); a call
  * whose 32-token chunk still needs more returns LGH_ERR_SHAPE.  The routes of
  * 1-64 tokens (and the 64-token chunks of a matrix too large for a GEMM
  * image) take their scratch in one piece and return LGH_ERR_SHAPE when it
@@ -294,9 +295,10 @@ int lgh_silu_mul_dev(lgh_ctx *ctx, float *g_dev, const float *u_dev, size_t n);
  * follow the context's act-quant mode.  One token with dim <= 2048 runs two
  * fused launches (the second reads h's ActQ8 codes written by the first).
  * Otherwise the ops above run on the device one after another, except that
- * for 5 or more tokens the activation-image kernels of the two GEMMs form
- * the norm (from per-row scales, without writing the normed rows) and
- * silu(g) * u themselves; the results equal the op sequence's bit for bit.
+ * for 5 or more tokens the norm and the gate/up activation image are
+ * formed in one launch (the normed rows are not written) and the down
+ * projection's image kernel forms silu(g) * u itself; the results equal the
+ * op sequence's bit for bit.
  * No single reference function: it replaces the reference's sequence of
  * calls. */
 int lgh_q4_ffn_residual(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, const lgh_q4 *w2,
@@ -316,7 +318,7 @@ int lgh_q4_ffn_residual_dev(lgh_ctx *ctx, const lgh_q4 *w1, const lgh_q4 *w3, co
  * its prologue and one activation quantization shared by all matrices (as
  * gemv_q4_pair shares one, crates/llm-cpu/src/gemv_q4.rs:396-443); otherwise
  * rms_norm then one lgh_q4_gemm per matrix (for 5 or more tokens the norm is
- * applied inside the shared activation-image kernel, from per-row scales).
+ * applied by the launch that writes the shared activation image).
  * Results equal that sequence. */
 int lgh_q4_norm_gemv(lgh_ctx *ctx, size_t nmat, const lgh_q4 *const *w, const float *norm_w, float eps,
                      const float *hidden, float *const *y, size_t tokens, int mode);

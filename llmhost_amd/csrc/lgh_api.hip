@@ -897,9 +897,9 @@ static int materialize(lgh_ctx *ctx, const ActIn &in, size_t m, size_t k, const 
 // activation quantization of each route (the MMA image, the GEMM's operand
 // image) is done once and read by every matrix.  m == 1 and m <= 4 quantize
 // inside their kernels, per matrix.  The rows may be rms_norm(x) or
-// silu(x) * u (ActIn): the MMA and GEMM routes form them inside their image
-// kernels (the norm from row scales computed first, without writing the normed
-// rows), the others after one more launch that writes them out.
+// silu(x) * u (ActIn): the MMA and GEMM routes form them in the launch that
+// writes their activation image (the normed rows are never written), the
+// others after one more launch that writes them out.
 static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, int nmat, ActIn in,
                           float *const *y_dev, size_t m, int mode) {
   const size_t k = w[0]->k, bpr = w[0]->bpr;
@@ -908,7 +908,7 @@ static int gemm_multi_dev(lgh_ctx *ctx, const Ws &wsp, const lgh_q4 *const *w, i
   if (m == 0 || nmax == 0) return LGH_OK;
   if (!aligned16(in.x) || !aligned16(in.u) || !aligned16(in.nw))
     return fail(ctx, LGH_ERR_INVALID_ARG, "activation rows must be 16-byte aligned");
-  // The image kernels' elementwise step: silu(x) * u, or rms_norm (row scales first).
+  // The image launch's elementwise step: silu(x) * u, or rms_norm.
   lgh::ActPrologue pro;
   pro.u = in.nw ? nullptr : in.u;
   pro.nw = in.nw;
@@ -1039,7 +1039,7 @@ int lgh_q4_gemm_dev(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_
 // lgh_q4_gemm_dev with every scratch buffer taken from the device's fixed
 // scratch array instead of the context workspace: no allocation, no free, no
 // synchronisation.  On the GEMM route (65+ tokens) token chunks shrink until
-// their scratch fits, with the split count of the whole call; a call that
+// their scratch fits, with the plan of the whole call; a call that
 // needs more than the array holds even for 32 tokens, or whose route takes
 // its scratch in one piece (1-64 tokens), fails with LGH_ERR_SHAPE.
 int lgh_q4_gemm_dev_noalloc(lgh_ctx *ctx, const lgh_q4 *w, const float *x_dev, float *y_dev, size_t m, int mode) {
