@@ -291,3 +291,33 @@ def test_prefill_fusions_equal_op_sequence(gpu_ctx, oracle, dim, inter, t, per_r
     assert fused.tobytes() == seq.tobytes(), "FFN block differs from the op sequence"
     assert gu_fused[0].tobytes() == g2.tobytes() and gu_fused[1].tobytes() == u2.tobytes(), \
         "norm + projections differ from rms_norm then the projections"
+
+
+# Rows of more than 128 blocks: the launch that forms the norm and the activation image loads a
+# row in rounds of 128 blocks, so these cover its later rounds (one block in the last round at
+# K = 4128); odd block counts cover the padding block of the last pair or quad.
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("k,n,t", [(8288, 256, 20), (8288, 300, 70), (12320, 96, 130), (4128, 64, 5)])
+def test_norm_projections_long_rows_equal_op_sequence(gpu_ctx, k, n, t, per_row):
+    """norm + two projections over rows of 129-385 blocks, on the matrix-core batch route (5 and 20
+    tokens) and the GEMM route (70 and 130), equal rms_norm then the projections bit for bit."""
+    print(f"[norm long rows] k={k} n={n} t={t} per_row={per_row}", flush=True)
+    blocks = [synth.q4_blocks(700 + k + j, n, k) for j in range(2)]
+    w = [q4.Q4Matrix.from_blocks(n, k, b, gpu_ctx) for b in blocks]
+    hidden = (synth.activations(710 + t, t, k) * np.float32(2.0)).astype(np.float32).ravel()
+    nw = (1 + 0.2 * synth.normal_f32(711 + k, k)).astype(np.float32)
+    gpu_ctx.set_act_quant(q4.ActQuant.PerRow if per_row else q4.ActQuant.PerBlock)
+    try:
+        normed = np.zeros_like(hidden)
+        q4.rms_norm(hidden, nw, 1e-5, normed, gpu_ctx)
+        fused = [np.zeros(t * n, np.float32) for _ in range(2)]
+        q4.norm_gemv(w, nw, 1e-5, hidden, fused, t)
+        seq = [np.zeros(t * n, np.float32) for _ in range(2)]
+        q4.norm_gemv(w, None, 1e-5, normed, seq, t)
+    finally:
+        gpu_ctx.set_act_quant(q4.ActQuant.PerBlock)
+        for m in w:
+            m.free()
+    for j in range(2):
+        assert np.isfinite(fused[j]).all()
+        assert fused[j].tobytes() == seq[j].tobytes(), f"matrix {j}"
